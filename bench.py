@@ -1,0 +1,247 @@
+"""Benchmark of the north-star workload: Qwen2.5-7B-shaped batched decode (config C3).
+
+One step = one decode token for each of 16 sequences: for each of the 28 layers, the fused RoPE + FP16 KV append
+and the GQA split-K flash-decode attention over the paged cache (the per-layer pairs run back to back; the
+projections around them are outside this path). Lengths are drawn uniform in [1,024, 32,768] from the seed;
+the KV cache is pre-filled through the same append path with N(0,1) fp32 K/V. Inputs are resident in HBM when
+the timed region starts.
+
+Prints one JSON line: the whole-job tokens/s, the step's algorithmic HBM GB/s, the dominant kernel's roofline
+(decode attention, timed with HIP events on the cache's stream over the timed region) and the CPU baseline (the
+restatement of Qwen2CpuAttention timed on host threads over one layer of the same workload).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode attn+KV-append tokens/s, HBM GB/s (% of peak), 7B shape @32k ctx"
+PEAK_HBM_GBPS = 8000.0
+SEED = 20261201
+CONFIG_OFFSET = 3  # config C3
+LAYERS, HEADS, KV_HEADS, HEAD_DIM = 28, 28, 4, 128
+SEQUENCES = 16
+PAGE_TOKENS = 256
+GROWTH = 1024
+KV_BYTES_PER_TOKEN_LAYER = 2 * KV_HEADS * HEAD_DIM * 2  # K + V, FP16
+PROFILES = ROOT / "profiles"
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def lengths_for(seed: int) -> np.ndarray:
+    return np.random.default_rng(seed).integers(1024, 32768 + 1, size=SEQUENCES)
+
+
+def measured_traffic() -> dict | None:
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary, when it exists."""
+    path = PROFILES / "decode_attention_c3_traffic.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text())
+
+
+def prefill(cache, torch, lengths, generator, chunk=4096):
+    """Fills every sequence through step + append_rope in prompt chunks (N(0,1) fp32 rows)."""
+    width = (HEADS + 2 * KV_HEADS) * HEAD_DIM
+    buffer = torch.empty((chunk, width), device="cuda")
+    for slot, length in enumerate(lengths.tolist()):
+        for first in range(0, length, chunk):
+            count = min(chunk, length - first)
+            cache.step([(slot, p) for p in range(first, first + count)])
+            for layer in range(LAYERS):
+                rows = buffer[:count]
+                rows.normal_(generator=generator)
+                cache.append_rope(layer, rows)
+    torch.cuda.synchronize()
+
+
+def cpu_baseline(lengths, threads: int) -> dict:
+    """The reference CPU attention restated in C++ (oracle/), timed on host threads: one layer of one decode step
+    over the same lengths (FP16 pages widened exactly, Qwen2CpuAttention order), extrapolated to 28 layers."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_ffi import PagedCache, rope_table
+
+    max_positions = int(lengths.max()) + 1024
+    pages = int(sum(-(-(int(n) + 1) // PAGE_TOKENS) for n in lengths)) + SEQUENCES
+    cache = PagedCache(1, HEADS, KV_HEADS, HEAD_DIM, max_positions, PAGE_TOKENS, PAGE_TOKENS, 1, SEQUENCES, pages,
+                       4096)
+    cos, sin = rope_table(HEAD_DIM, 1e6, max_positions)
+    rng = np.random.default_rng(SEED + CONFIG_OFFSET)
+    width = (HEADS + 2 * KV_HEADS) * HEAD_DIM
+    start = time.perf_counter()
+    for slot, length in enumerate(lengths.tolist()):
+        assert cache.reserve(slot, length + 1) == 0
+        for first in range(0, length, 4096):
+            count = min(4096, length - first)
+            rows = np.zeros((count, width), dtype=np.float32)
+            rows[:, HEADS * HEAD_DIM:] = rng.standard_normal((count, 2 * KV_HEADS * HEAD_DIM), dtype=np.float32)
+            assert cache.step([(slot, p) for p in range(first, first + count)]) == 0
+            assert cache.append_rope(0, rows, cos, sin) == 0
+    fill_seconds = time.perf_counter() - start
+    tokens = [(slot, int(length)) for slot, length in enumerate(lengths)]
+    assert cache.step(tokens) == 0
+    rows = rng.standard_normal((SEQUENCES, width), dtype=np.float32)
+    assert cache.append_rope(0, rows, cos, sin) == 0
+    out = np.zeros((SEQUENCES, HEADS * HEAD_DIM), dtype=np.float32)
+    cache.attention(0, rows, out, threads)  # warm-up
+    times = [cache.attention(0, rows, out, threads) for _ in range(3)]
+    layer_seconds = statistics.median(times)
+    step_seconds = layer_seconds * LAYERS
+    return {
+        "value": SEQUENCES / step_seconds,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"decode attention of one layer for the 16 drawn lengths (sum {int(lengths.sum())} keys), median of 3 "
+            f"after 1 warm-up, x28 layers; C++ restatement of Qwen2CpuAttention (4-lane dot, 3-pass softmax) over "
+            f"FP16 pages widened per Fp16.ToSingle, {threads} std::threads; append excluded; fill took "
+            f"{fill_seconds:.1f} s"
+        ),
+        "ms_per_layer": layer_seconds * 1e3,
+    }
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--split-keys", type=int, default=None)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-threads", type=int, default=None)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the decode shards by sequence with no exchange, so N GPUs would run N independent copies.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from synapse_amd import PagedKvCache
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a HIP device")
+    torch.cuda.set_device(0)
+    lengths = lengths_for(SEED + CONFIG_OFFSET)
+    total_steps = args.warmup + args.steps
+    max_positions = int(-(-(int(lengths.max()) + total_steps + 1) // GROWTH) * GROWTH)
+    reserved = [-(-(int(n) + total_steps + 1) // GROWTH) * GROWTH for n in lengths]
+    pages = sum(-(-r // PAGE_TOKENS) for r in reserved)
+    log(f"lengths {lengths.tolist()} sum {int(lengths.sum())}; pages {pages}")
+    cache = PagedKvCache(layers=LAYERS, heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM,
+                         max_positions=max_positions, growth_positions=GROWTH, page_tokens=PAGE_TOKENS,
+                         precision="f16", session_slots=SEQUENCES, step_tokens=4096, max_pages=pages)
+    stream = torch.cuda.current_stream()
+    cache.set_stream(stream)
+    if args.split_keys:
+        cache.set_split_keys(args.split_keys)
+    for slot, length in enumerate(lengths.tolist()):
+        cache.reserve(slot, length + total_steps + 1)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(SEED + CONFIG_OFFSET)
+    started = time.perf_counter()
+    prefill(cache, torch, lengths, generator)
+    log(f"prefill {time.perf_counter() - started:.1f} s; KV bytes {cache.allocated_bytes / 2**30:.2f} GiB")
+
+    width = (HEADS + 2 * KV_HEADS) * HEAD_DIM
+    qkv = torch.empty((LAYERS, SEQUENCES, width), device="cuda").normal_(generator=generator)
+    out = torch.empty((LAYERS, SEQUENCES, HEADS * HEAD_DIM), device="cuda")
+
+    def step(index: int, events=None) -> None:
+        cache.step([(slot, int(lengths[slot]) + index) for slot in range(SEQUENCES)])
+        for layer in range(LAYERS):
+            cache.append_rope(layer, qkv[layer])
+            if events is not None:
+                events[layer][0].record(stream)
+            cache.attention(layer, qkv[layer], out[layer])
+            if events is not None:
+                events[layer][1].record(stream)
+
+    for index in range(args.warmup):
+        step(index)
+    torch.cuda.synchronize()
+    timed_events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                     for _ in range(LAYERS)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    begin = time.perf_counter()
+    for index in range(args.steps):
+        step(args.warmup + index, timed_events[index])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - begin
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    tokens_per_second = SEQUENCES * args.steps / elapsed
+    # Algorithmic bytes: each step reads the K/V of every attended position once per layer and writes the new
+    # token's K/V; q/out rows are read/written once (fp32).
+    keys_per_step = [int((lengths + args.warmup + index + 1).sum()) for index in range(args.steps)]
+    qo_bytes = 2 * SEQUENCES * HEADS * HEAD_DIM * 4
+    append_bytes = SEQUENCES * (KV_BYTES_PER_TOKEN_LAYER + 2 * (HEADS + 2 * KV_HEADS) * HEAD_DIM * 4)
+    attention_bytes = [keys * KV_BYTES_PER_TOKEN_LAYER + qo_bytes for keys in keys_per_step]
+    step_bytes = [LAYERS * (b + append_bytes) for b in attention_bytes]
+    step_gbps = sum(step_bytes) / elapsed / 1e9
+    durations = [start.elapsed_time(end) * 1e-3 for step_events in timed_events for start, end in step_events]
+    attention_seconds = statistics.mean(durations)
+    attention_gbps = statistics.mean(attention_bytes) / attention_seconds / 1e9
+    traffic = measured_traffic()
+
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_second, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": f"synthetic: N(0,1) fp32 q/k/v from torch seed {SEED + CONFIG_OFFSET}, KV pre-filled through the "
+                f"append path; lengths from numpy default_rng({SEED + CONFIG_OFFSET})",
+        "config": {
+            "workload": "C3: Qwen2.5-7B-shaped batched decode, 16 sequences, ragged lengths U[1024, 32768], "
+                        "FP16 paged KV (256-token pages), append + flash-decode per layer, 28 layers",
+            "layers": LAYERS, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM, "sequences": SEQUENCES,
+            "page_tokens": PAGE_TOKENS, "lengths": lengths.tolist(), "parallelism": "single GPU",
+        },
+        "hbm_gbps": round(step_gbps, 1),
+        "hbm_frac_of_peak": round(step_gbps / PEAK_HBM_GBPS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode attention (decode_f16_kernel<128> + split merge) per layer",
+            "achieved": round(attention_gbps, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(attention_gbps / PEAK_HBM_GBPS, 4),
+            "traffic": traffic["bytes_per_launch"] if traffic else None,
+            "algorithmic_bytes_per_launch": int(statistics.mean(attention_bytes)),
+            "avg_launch_us": round(attention_seconds * 1e6, 2),
+        },
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"cpu baseline on {threads} threads")
+        baseline = cpu_baseline(lengths, threads)
+        result["cpu_baseline"] = baseline
+    cache.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

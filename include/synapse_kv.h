@@ -1,0 +1,201 @@
+/*
+ * libsynapse_kv: the KV-cache and attention hot path of Synapse's decoder step on AMD Instinct MI355X (gfx950).
+ *
+ * A versioned C ABI with the conventions of Synapse's GPU library (native/synapse-gpu/src/Features/GpuKernels/
+ * ffi.rs:1-263): every entry point validates its pointers, catches C++ exceptions, returns a status code and
+ * records a thread-local message that synapse_kv_last_error copies out. A cache handle must not be used by two
+ * threads at once (ffi.rs:177-180).
+ *
+ * Ownership: the caller owns the RoPE tables (copied to the device at create, as DecoderDesc.rope_cosines/sines,
+ * decoder.rs:102-103), the token array and every qkv/output buffer. The cache owns its device page pool, block
+ * tables, reference counts and free stack. qkv and output pointers are device pointers (HIP-resident step);
+ * host-side arrays are passed only where noted. All device work is ordered on the cache's stream.
+ *
+ * Every struct below has its size pinned with a static assertion here and in the C# binding.
+ */
+#ifndef SYNAPSE_KV_H
+#define SYNAPSE_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version checked by the loader before any other call (ffi.rs:12 ABI_VERSION; NativeGpuLibrary.cs:14). */
+#define SYNAPSE_KV_ABI_VERSION 1u
+
+/* Status codes, identical to error.rs:4-16. */
+#define SYNAPSE_KV_OK 0
+#define SYNAPSE_KV_NULL_POINTER 1
+#define SYNAPSE_KV_INVALID_ARGUMENT 2
+#define SYNAPSE_KV_UNAVAILABLE 3
+#define SYNAPSE_KV_DEVICE_ERROR 4
+#define SYNAPSE_KV_OUT_OF_MEMORY 5
+#define SYNAPSE_KV_PANIC 6
+
+/* KV element types, values as KV_F32 / KV_F16 (decoder.rs:37-39). */
+#define SYNAPSE_KV_F32 0u
+#define SYNAPSE_KV_F16 1u
+
+/* Tuning options for synapse_kv_set_option. */
+#define SYNAPSE_KV_OPTION_SPLIT_KEYS 1u     /* keys per decode split-K work item; a multiple of 64 (default 512) */
+#define SYNAPSE_KV_OPTION_PREFILL_RUNS 2u   /* 1: FP16 prompt runs use the MFMA prefill kernel (default); 0: decode path */
+#define SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS 3u /* keys per prefill split-K work item; a multiple of 64 (default 16384) */
+
+/* GpuDeviceInfo (native/synapse-gpu/src/Features/GpuKernels/mod.rs:20-31), 152 bytes. */
+typedef struct SynapseKvDeviceInfo {
+    uint8_t name[128];
+    uint64_t recommended_working_set_bytes;
+    uint64_t max_buffer_bytes;
+    uint32_t unified_memory;
+    uint32_t apple_family;
+} SynapseKvDeviceInfo;
+
+/* BatchToken (decoder.rs:133-141), 16 bytes: the C# BatchToken array passes through unchanged. `slot` is the
+ * sequence, `position` the KV position the token writes and attends up to (inclusive); token and logits_row are
+ * carried but not read by this library. */
+typedef struct SynapseKvBatchToken {
+    int32_t slot;
+    int32_t token;
+    int32_t position;
+    int32_t logits_row;
+} SynapseKvBatchToken;
+
+/* Cache description: the KV-relevant part of DecoderDesc (decoder.rs:95-128), 64 bytes.
+ * layer_count counts executed layers only: dropped layers get no KV (ADR-019; Qwen2ModelComposition.cs:13-36).
+ * page_tokens is a multiple of 64 in 64..1024; kv_growth_positions a positive multiple of page_tokens (the
+ * reference requires a multiple of 64, decoder/checks.rs); max_pages sizes the device page pool. */
+typedef struct SynapseKvDesc {
+    const float* rope_cosines; /* host, [max_positions][head_dim / 2] */
+    const float* rope_sines;   /* host, [max_positions][head_dim / 2] */
+    uint32_t layer_count;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim; /* 64 or 128 (METAL_HEAD_DIMS, decoder.rs:23) */
+    uint32_t max_positions;
+    uint32_t kv_growth_positions;
+    uint32_t page_tokens;
+    uint32_t kv_precision;
+    uint32_t session_slots;
+    uint32_t step_tokens;
+    uint32_t max_pages;
+    int32_t device;
+} SynapseKvDesc;
+
+/* Page pool occupancy, 40 bytes. */
+typedef struct SynapseKvPageStats {
+    uint32_t max_pages;
+    uint32_t free_pages;
+    uint32_t used_pages;
+    uint32_t shared_pages; /* pages with a reference count above one */
+    uint64_t page_bytes;
+    uint64_t kv_bytes; /* used_pages * page_bytes */
+    uint32_t device_status; /* 0, or the first inconsistency the table kernel found */
+    uint32_t reserved;
+} SynapseKvPageStats;
+
+typedef struct SynapseKvCache SynapseKvCache;
+
+/* synapse_gpu_abi_version (ffi.rs:53-57). */
+uint32_t synapse_kv_abi_version(void);
+
+/* synapse_gpu_probe (ffi.rs:59-80) for the current HIP device. */
+int32_t synapse_kv_probe(SynapseKvDeviceInfo* info);
+
+/* synapse_gpu_last_error (ffi.rs:86-104): copies the calling thread's last message (UTF-8, not terminated) and
+ * returns its full length. */
+size_t synapse_kv_last_error(uint8_t* buffer, size_t capacity);
+
+/* synapse_gpu_decoder_create (ffi.rs:106-142) for the KV path: validates the shape, copies the RoPE tables and
+ * allocates the page pool. */
+int32_t synapse_kv_cache_create(const SynapseKvDesc* desc, SynapseKvCache** cache);
+
+/* synapse_gpu_decoder_destroy (ffi.rs:215-227); null is ignored. */
+void synapse_kv_cache_destroy(SynapseKvCache* cache);
+
+/* Orders all later device work of the cache on `stream` (a hipStream_t; null = the default stream). */
+int32_t synapse_kv_set_stream(SynapseKvCache* cache, void* stream);
+
+/* Tuning knobs (SYNAPSE_KV_OPTION_*). */
+int32_t synapse_kv_set_option(SynapseKvCache* cache, uint32_t option, uint32_t value);
+
+/* synapse_gpu_decoder_kv_bytes (ffi.rs:229-248): bytes of the pages in use, shared pages counted once;
+ * 0 for null. */
+uint64_t synapse_kv_bytes(const SynapseKvCache* cache);
+
+/* synapse_gpu_decoder_reserve (ffi.rs:250-263) / MetalDecoder::reserve (metal/decoder.rs:164-179) with the
+ * Qwen2KvCache.Reserve policy (Qwen2KvCache.cs:56-72): grow to the rounded need, or contract when the rounded
+ * need is at most a quarter of the capacity; the prefix is kept. */
+int32_t synapse_kv_reserve(SynapseKvCache* cache, uint32_t slot, uint32_t positions);
+
+/* Qwen2KvCache.Release (Qwen2KvCache.cs:75-84) / Qwen2KvSlots.Release (Qwen2Vectors.cs:39-53) for one slot. */
+int32_t synapse_kv_release(SynapseKvCache* cache, uint32_t slot);
+
+/* Rollback to a shorter committed length (kv_pages.rs:158-177; DirectSessionPrefix.Claim forgetting,
+ * DirectSessionPrefix.cs:16-27). Capacity is kept. */
+int32_t synapse_kv_truncate(SynapseKvCache* cache, uint32_t slot, uint32_t length);
+
+/* Prefix reuse across slots (ADR-018 extended to copy-on-write): the empty `target` shares every page that holds
+ * `source`'s written positions. */
+int32_t synapse_kv_fork(SynapseKvCache* cache, uint32_t source, uint32_t target);
+
+/* Starts a step (MetalDecoder::forward's prepare_slots + plan_attention, metal/decoder.rs:106-156): validates
+ * the tokens (validate_step, decoder.rs:303-335), grows slots and copies shared pages on write, and uploads the
+ * tokens and the attention work plan. `tokens` is a host array. */
+int32_t synapse_kv_step(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count);
+
+/* synapse_rope_kv[_f16] for one layer of the current step (elementwise.metal:73-126; dispatch step/layers.rs:
+ * 111-148): `qkv` is a device [tokens][qkv_stride] FP32 block with Q at column 0, K at heads*head_dim and V at
+ * (heads + kv_heads)*head_dim. Q and K rotate in place; K and V are appended to the pages (FP16: round to nearest
+ * even). */
+int32_t synapse_kv_append_rope(SynapseKvCache* cache, uint32_t layer, float* qkv, uint32_t qkv_stride);
+
+/* Attention of the current step for one layer (step/attention.rs:9-145: synapse_attention for prompt runs,
+ * synapse_attention_decode + synapse_attention_reduce for lone tokens): every token attends keys
+ * 0..position of its slot. Reads Q from `qkv` (device), writes [tokens][out_stride] FP32 `output` (device)
+ * at column head*head_dim. */
+int32_t synapse_kv_attention(SynapseKvCache* cache, uint32_t layer, const float* qkv, uint32_t qkv_stride,
+                             float* output, uint32_t out_stride);
+
+/* Waits for the cache's stream. */
+int32_t synapse_kv_synchronize(SynapseKvCache* cache);
+
+/* Host-side view of a slot: capacity (positions), written length and mapped pages. */
+int32_t synapse_kv_slot_info(const SynapseKvCache* cache, uint32_t slot, uint32_t* capacity, uint32_t* length,
+                             uint32_t* pages);
+
+/* Device state read-back for bit-exact checks (synchronous; host output arrays). */
+int32_t synapse_kv_read_block_table(SynapseKvCache* cache, uint32_t slot, int32_t* pages, size_t capacity,
+                                    size_t* count);
+int32_t synapse_kv_read_refcounts(SynapseKvCache* cache, int32_t* counts, size_t capacity);
+int32_t synapse_kv_read_free_list(SynapseKvCache* cache, int32_t* pages, size_t capacity, size_t* count);
+int32_t synapse_kv_page_stats(SynapseKvCache* cache, SynapseKvPageStats* stats);
+
+/* Copies positions [first, first + count) of one slot and layer into host arrays as [position][kv_head][head_dim]
+ * in the storage type (float or uint16 FP16 bits): GetKey/GetValue (Qwen2KvCache.cs:86-88) in bulk. */
+int32_t synapse_kv_read_kv(SynapseKvCache* cache, uint32_t slot, uint32_t layer, uint32_t first, uint32_t count,
+                           void* keys, void* values);
+
+/* RopeFrequencies (RopeFrequencies.cs:20-81) into host [positions][head_dim / 2] tables; yarn_factor <= 0 means
+ * unscaled. The C# host builds the same tables itself (GpuDecoderExecutor.BuildRopeTables,
+ * GpuDecoderExecutor.cs:183-192). */
+int32_t synapse_kv_rope_table(uint32_t head_dim, float theta, float yarn_factor, uint32_t yarn_original,
+                              uint32_t positions, float* cosines, float* sines);
+
+#ifdef __cplusplus
+} /* extern "C" */
+
+static_assert(sizeof(SynapseKvDeviceInfo) == 152, "SynapseKvDeviceInfo is pinned at 152 bytes");
+static_assert(sizeof(SynapseKvBatchToken) == 16, "SynapseKvBatchToken is pinned at 16 bytes");
+static_assert(sizeof(SynapseKvDesc) == 64, "SynapseKvDesc is pinned at 64 bytes");
+static_assert(sizeof(SynapseKvPageStats) == 40, "SynapseKvPageStats is pinned at 40 bytes");
+#else
+_Static_assert(sizeof(SynapseKvDeviceInfo) == 152, "SynapseKvDeviceInfo is pinned at 152 bytes");
+_Static_assert(sizeof(SynapseKvBatchToken) == 16, "SynapseKvBatchToken is pinned at 16 bytes");
+_Static_assert(sizeof(SynapseKvDesc) == 64, "SynapseKvDesc is pinned at 64 bytes");
+_Static_assert(sizeof(SynapseKvPageStats) == 40, "SynapseKvPageStats is pinned at 40 bytes");
+#endif
+
+#endif /* SYNAPSE_KV_H */

@@ -1,0 +1,130 @@
+// Fused RoPE + KV append (synapse_rope_kv, native/synapse-gpu/src/Features/GpuKernels/metal/shaders/
+// elementwise.metal:73-126): rotate Q in place, rotate K in place and store it, store V, converting to the page's
+// element type (FP16: round to nearest even, v_cvt_f16_f32 in the default rounding mode).
+// The rotation follows Qwen2RopeTable.Apply (src/Synapse.Runtime/Features/TextGeneration/Qwen2/
+// Qwen2CpuState.cs:85-106): x' = x*c - y*s, y' = x*s + y*c with every product and sum rounded separately (no
+// fused multiply-add), so the result is bit-exact with the CPU path.
+//
+// One workgroup per token. K rows are stored with consecutive lanes on consecutive dims; V is stored transposed
+// ([dim][position] per page region), one 2- or 4-byte store per dim.
+
+#include "kv_internal.h"
+
+namespace synapse_kv {
+namespace {
+
+template <typename T>
+__device__ inline T to_storage(float value);
+
+template <>
+__device__ inline float to_storage<float>(float value) {
+    return value;
+}
+
+template <>
+__device__ inline _Float16 to_storage<_Float16>(float value) {
+    return static_cast<_Float16>(value);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+    const Geometry& g = a.geo;
+    const int index = blockIdx.x;
+    const SynapseKvBatchToken token = a.tokens[index];
+    float* row = a.qkv + static_cast<size_t>(index) * a.qkv_stride;
+    const int half = a.half_dim;
+    const int d = g.head_dim;
+    const float* cosines = a.cosines + static_cast<size_t>(token.position) * half;
+    const float* sines = a.sines + static_cast<size_t>(token.position) * half;
+    const int logical = token.position / g.page_tokens;
+    const int within = token.position - logical * g.page_tokens;
+    const int page = g.block_table[static_cast<size_t>(token.slot) * g.pages_per_slot + logical];
+    T* base = reinterpret_cast<T*>(a.pool + static_cast<uint64_t>(page) * g.page_bytes);
+    const size_t region = static_cast<size_t>(g.page_tokens) * d;
+    const size_t layer_base = static_cast<size_t>(g.layer) * 2 * g.kv_heads;
+
+    const int rotations = (g.heads + g.kv_heads) * half;
+    for (int item = threadIdx.x; item < rotations; item += blockDim.x) {
+        const int head = item / half;
+        const int i = item - head * half;
+        float* values = row + static_cast<size_t>(head) * d;  // K heads follow the Q heads in the row
+        const float x = values[i];
+        const float y = values[i + half];
+        const float c = cosines[i];
+        const float s = sines[i];
+        const float first = __fsub_rn(__fmul_rn(x, c), __fmul_rn(y, s));
+        const float second = __fadd_rn(__fmul_rn(x, s), __fmul_rn(y, c));
+        values[i] = first;
+        values[i + half] = second;
+        if (head >= g.heads) {
+            const int kv_head = head - g.heads;
+            T* keys = base + (layer_base + kv_head) * region + static_cast<size_t>(within) * d;
+            keys[i] = to_storage<T>(first);
+            keys[i + half] = to_storage<T>(second);
+        }
+    }
+
+    const float* value_row = row + static_cast<size_t>(g.heads + g.kv_heads) * d;
+    const int stores = g.kv_heads * d;
+    for (int item = threadIdx.x; item < stores; item += blockDim.x) {
+        const int kv_head = item / d;
+        const int dim = item - kv_head * d;
+        T* values = base + (layer_base + g.kv_heads + kv_head) * region;
+        values[static_cast<size_t>(dim) * g.page_tokens + within] = to_storage<T>(value_row[item]);
+    }
+}
+
+// Reads positions [first, first + count) of one slot/layer back into [position][kv_head][dim] order.
+template <typename T>
+__global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
+    const Geometry& g = a.geo;
+    const int d = g.head_dim;
+    const size_t per_position = static_cast<size_t>(g.kv_heads) * d;
+    const size_t total = per_position * a.count;
+    const size_t region = static_cast<size_t>(g.page_tokens) * d;
+    const size_t layer_base = static_cast<size_t>(g.layer) * 2 * g.kv_heads;
+    for (size_t index = blockIdx.x * 256ull + threadIdx.x; index < total; index += gridDim.x * 256ull) {
+        const int position = a.first + static_cast<int>(index / per_position);
+        const int kv_head = static_cast<int>((index % per_position) / d);
+        const int dim = static_cast<int>(index % d);
+        const int logical = position / g.page_tokens;
+        const int within = position - logical * g.page_tokens;
+        const int page = g.block_table[static_cast<size_t>(a.slot) * g.pages_per_slot + logical];
+        const T* base = reinterpret_cast<const T*>(g.pool + static_cast<uint64_t>(page) * g.page_bytes);
+        const T key = base[(layer_base + kv_head) * region + static_cast<size_t>(within) * d + dim];
+        const T value = base[(layer_base + g.kv_heads + kv_head) * region + static_cast<size_t>(dim) * g.page_tokens + within];
+        reinterpret_cast<T*>(a.keys)[index] = key;
+        reinterpret_cast<T*>(a.values)[index] = value;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_append(hipStream_t stream, const AppendArgs& args, int tokens, bool fp16) {
+    if (tokens == 0) {
+        return hipSuccess;
+    }
+    if (fp16) {
+        hipLaunchKernelGGL(append_kernel<_Float16>, dim3(tokens), dim3(256), 0, stream, args);
+    } else {
+        hipLaunchKernelGGL(append_kernel<float>, dim3(tokens), dim3(256), 0, stream, args);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(hipStream_t stream, const GatherArgs& args, bool fp16) {
+    const size_t total = static_cast<size_t>(args.geo.kv_heads) * args.geo.head_dim * args.count;
+    if (total == 0) {
+        return hipSuccess;
+    }
+    const size_t blocks = (total + 255) / 256;
+    const dim3 grid(static_cast<unsigned>(blocks < 4096 ? blocks : 4096));
+    if (fp16) {
+        hipLaunchKernelGGL(gather_kernel<_Float16>, grid, dim3(256), 0, stream, args);
+    } else {
+        hipLaunchKernelGGL(gather_kernel<float>, grid, dim3(256), 0, stream, args);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace synapse_kv

@@ -1,0 +1,218 @@
+// Chunked-prefill (prompt-run) attention on FP16 MFMA.
+//
+// Semantics: synapse_attention for prompt runs (native/synapse-gpu/src/Features/GpuKernels/metal/shaders/
+// attention.metal:254-313; dispatch step/attention.rs:62-104): consecutive tokens of one slot at consecutive
+// positions attend causally, token j sees keys 0..position_j (mask `key <= row_position`, attention.metal:80-81),
+// after the run's K/V were appended (step/layers.rs:95-96). Long runs split their keys across work items and
+// merge with the decode merge kernel (same (max, sum) partial rows).
+//
+// MI355X mapping: one workgroup per (KV head, block of kPrefillTokens tokens, key split) with one wave per query
+// head of the GQA group, so the group's waves read the same K/V lines together. Each wave holds its head's
+// queries for the block as kPrefillTiles MFMA column tiles of 16 tokens and runs the decode kernel's 64-key step:
+// S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16, every K/V fragment loaded once and used by all
+// column tiles. Causal masking is a per-element compare against the column's position.
+
+#include "kv_internal.h"
+
+namespace synapse_kv {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr float kNegativeInfinity = -__builtin_inff();
+
+__device__ inline float fast_exp2(float value) { return __builtin_amdgcn_exp2f(value); }
+
+template <int D>
+__global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
+    constexpr int NT = kPrefillTiles;
+    const PrefillItem item = a.prefill[blockIdx.x];
+    const Geometry& geo = a.geo;
+    const int wave = threadIdx.x >> 6;  // query head within the group
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int head = item.kv_head * geo.group + wave;
+    const SynapseKvBatchToken first = a.tokens[item.first_token];
+    const int first_position = first.position;
+
+    // B operands of S^T = K Q^T: tile c, lane (g, r) holds dims 32*ks + 8*g .. +7 of token 16*c + r.
+    half8 query[NT][D / 32];
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+        const int j = 16 * c + r;
+        const bool valid = j < item.count;
+        const float* q = a.qkv + static_cast<size_t>(item.first_token + (valid ? j : 0)) * a.qkv_stride +
+                         static_cast<size_t>(head) * D;
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const floatx4 lo = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g);
+            const floatx4 hi = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                query[c][ks][e] = valid ? static_cast<_Float16>(lo[e]) : static_cast<_Float16>(0.0f);
+                query[c][ks][e + 4] = valid ? static_cast<_Float16>(hi[e]) : static_cast<_Float16>(0.0f);
+            }
+        }
+    }
+
+    floatx4 out[NT][D / 16];
+    float maximum[NT];
+    float sum[NT];
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+#pragma unroll
+        for (int mt = 0; mt < D / 16; ++mt) {
+            out[c][mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        maximum[c] = kNegativeInfinity;
+        sum[c] = 0.0f;
+    }
+
+    const int32_t* table = geo.block_table + static_cast<size_t>(first.slot) * geo.pages_per_slot;
+    const size_t region = static_cast<size_t>(geo.page_tokens) * D;
+    const size_t key_region = ((static_cast<size_t>(geo.layer) * 2) * geo.kv_heads + item.kv_head) * region;
+    const size_t value_region = ((static_cast<size_t>(geo.layer) * 2 + 1) * geo.kv_heads + item.kv_head) * region;
+    const int page_tokens = geo.page_tokens;
+    const int row_key = 8 * (r >> 2) + (r & 3);
+    // Keys past the block's last token are masked for every column.
+    const int key_stop = min(item.key_end, first_position + item.count);
+
+    for (int key0 = item.key_begin; key0 < key_stop; key0 += kStepKeys) {
+        const int logical = key0 / page_tokens;
+        const int within = key0 - logical * page_tokens;
+        const _Float16* page = reinterpret_cast<const _Float16*>(
+            geo.pool + static_cast<uint64_t>(table[logical]) * geo.page_bytes);
+        const _Float16* keys = page + key_region + static_cast<size_t>(within) * D;
+        const _Float16* values = page + value_region + within;
+
+        floatx4 scores[NT][4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int key = 32 * (t >> 1) + row_key + 4 * (t & 1);
+            half8 fragment[D / 32];
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+                fragment[ks] = *reinterpret_cast<const half8*>(keys + static_cast<size_t>(key) * D + 32 * ks + 8 * g);
+            }
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+                scores[c][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int ks = 0; ks < D / 32; ++ks) {
+                    scores[c][t] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(fragment[ks], query[c][ks], scores[c][t], 0, 0, 0);
+                }
+            }
+        }
+
+        half8 probability[NT][2];
+        float alpha[NT];
+#pragma unroll
+        for (int c = 0; c < NT; ++c) {
+            const int column_position = first_position + 16 * c + r;
+            float tile_max = kNegativeInfinity;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = key0 + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
+                    const bool visible = key < item.key_end && key <= column_position;
+                    const float s = visible ? scores[c][t][i] * a.scale_log2 : kNegativeInfinity;
+                    scores[c][t][i] = s;
+                    tile_max = fmaxf(tile_max, s);
+                }
+            }
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+            const float next = fmaxf(maximum[c], tile_max);
+            // A column may see no key of this split yet; keep its state at (-inf, 0) without NaN.
+            const float base = next == kNegativeInfinity ? 0.0f : next;
+            alpha[c] = fast_exp2(maximum[c] - base);
+            float tile_sum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = fast_exp2(scores[c][t][i] - base);
+                    tile_sum += p;
+                    probability[c][t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(p);
+                }
+            }
+            sum[c] = sum[c] * alpha[c] + tile_sum;
+            maximum[c] = next;
+        }
+#pragma unroll
+        for (int mt = 0; mt < D / 16; ++mt) {
+            half8 value_fragment[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                value_fragment[h] = *reinterpret_cast<const half8*>(
+                    values + static_cast<size_t>(16 * mt + r) * page_tokens + 32 * h + 8 * g);
+            }
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+                out[c][mt] *= alpha[c];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    out[c][mt] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(value_fragment[h], probability[c][h], out[c][mt], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    const int group = geo.group;
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+        float total = sum[c];
+        total += __shfl_xor(total, 16);
+        total += __shfl_xor(total, 32);
+        const int j = 16 * c + r;
+        if (j >= item.count) {
+            continue;
+        }
+        const int token = item.first_token + j;
+        if (item.row < 0) {
+            float* destination = a.output + static_cast<size_t>(token) * a.out_stride + static_cast<size_t>(head) * D;
+            const float inverse = 1.0f / total;
+#pragma unroll
+            for (int mt = 0; mt < D / 16; ++mt) {
+                *reinterpret_cast<floatx4*>(destination + 16 * mt + 4 * g) = out[c][mt] * inverse;
+            }
+        } else {
+            const size_t row = static_cast<size_t>(item.row + j * item.row_stride) * group + wave;
+            float* destination = a.partial_out + row * D;
+#pragma unroll
+            for (int mt = 0; mt < D / 16; ++mt) {
+                *reinterpret_cast<floatx4*>(destination + 16 * mt + 4 * g) = out[c][mt];
+            }
+            if (g == 0) {
+                a.partial_ml[row * 2] = maximum[c];
+                a.partial_ml[row * 2 + 1] = total;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_prefill(hipStream_t stream, const AttentionArgs& args, int items, bool fp16) {
+    if (items == 0) {
+        return hipSuccess;
+    }
+    if (!fp16) {
+        return hipErrorNotSupported;  // the planner sends FP32 prompt runs through the decode kernel
+    }
+    const dim3 grid(items);
+    const dim3 block(args.geo.group * 64);
+    if (args.geo.head_dim == 128) {
+        hipLaunchKernelGGL(prefill_f16_kernel<128>, grid, block, 0, stream, args);
+    } else {
+        hipLaunchKernelGGL(prefill_f16_kernel<64>, grid, block, 0, stream, args);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace synapse_kv

@@ -1,0 +1,1070 @@
+// Host half of libsynapse_kv: the C ABI, argument validation, the capacity policy, a host shadow of the page
+// allocator (used to reject a call before any device work and to size launches without reading the device back),
+// the per-step attention plan, and the kernel launches.
+//
+// ABI conventions follow native/synapse-gpu/src/Features/GpuKernels/ffi.rs: status codes (error.rs:4-16), a
+// thread-local last error copied out by length (ffi.rs:19, 86-104), every entry point guarded (ffi.rs:34-45,
+// C++ exceptions here instead of Rust panics), opaque handles, null-safe destroy and kv_bytes.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "kv_internal.h"
+
+namespace synapse_kv {
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Failure {
+    int32_t status;
+    std::string message;
+};
+
+[[noreturn]] void fail(int32_t status, const std::string& message) { throw Failure{status, message}; }
+
+[[noreturn]] void invalid(const std::string& message) { fail(SYNAPSE_KV_INVALID_ARGUMENT, "invalid argument: " + message); }
+
+void check_hip(hipError_t error, const char* what) {
+    if (error == hipSuccess) {
+        return;
+    }
+    const int32_t status = error == hipErrorOutOfMemory ? SYNAPSE_KV_OUT_OF_MEMORY : SYNAPSE_KV_DEVICE_ERROR;
+    fail(status, std::string(status == SYNAPSE_KV_OUT_OF_MEMORY ? "out of device memory: " : "device error: ") + what +
+                     ": " + hipGetErrorString(error));
+}
+
+int32_t record(int32_t status, const std::string& message) {
+    g_last_error = message;
+    return status;
+}
+
+template <typename Body>
+int32_t guarded(Body body) {
+    try {
+        body();
+        return SYNAPSE_KV_OK;
+    } catch (const Failure& failure) {
+        return record(failure.status, failure.message);
+    } catch (const std::bad_alloc&) {
+        return record(SYNAPSE_KV_OUT_OF_MEMORY, "out of host memory");
+    } catch (const std::exception& error) {
+        return record(SYNAPSE_KV_PANIC, std::string("a C++ exception was caught at the KV ABI: ") + error.what());
+    } catch (...) {
+        return record(SYNAPSE_KV_PANIC, "a C++ exception was caught at the KV ABI");
+    }
+}
+
+// Qwen2KvCache.NextCapacity (Qwen2KvCache.cs:91-95) = DecoderShape::next_capacity (decoder.rs:221-226).
+uint32_t next_capacity(uint32_t needed, uint32_t current, uint32_t growth, uint32_t maximum) {
+    const uint64_t rounded = std::min<uint64_t>(maximum, (static_cast<uint64_t>(needed) + growth - 1) / growth * growth);
+    return static_cast<uint32_t>(
+        std::min<uint64_t>(maximum, std::max<uint64_t>(rounded, std::min<uint64_t>(maximum, 2ull * current))));
+}
+
+// Reservation rounding (Qwen2KvCache.cs:63; DecoderShape::reserve_capacity, decoder.rs:207-216).
+uint32_t reserve_rounded(uint32_t positions, uint32_t growth, uint32_t maximum) {
+    return static_cast<uint32_t>(
+        std::min<uint64_t>(maximum, (static_cast<uint64_t>(positions) + growth - 1) / growth * growth));
+}
+
+template <typename T>
+struct DeviceBuffer {
+    T* pointer = nullptr;
+    size_t count = 0;
+
+    void reset() {
+        if (pointer != nullptr) {
+            (void)hipFree(pointer);
+        }
+        pointer = nullptr;
+        count = 0;
+    }
+
+    // Grows to at least `wanted` elements (contents are not kept). Work already queued may still read the old
+    // buffer, so the device is drained before it is freed.
+    void ensure(size_t wanted, const char* what) {
+        if (wanted <= count) {
+            return;
+        }
+        if (pointer != nullptr) {
+            check_hip(hipDeviceSynchronize(), "drain before reallocation");
+        }
+        reset();
+        check_hip(hipMalloc(reinterpret_cast<void**>(&pointer), std::max<size_t>(wanted, 1) * sizeof(T)), what);
+        count = wanted;
+    }
+};
+
+// Two pinned host staging buffers used alternately for host-to-device uploads; an event per buffer tells when
+// its last copy finished, so a buffer is never rewritten while the device may still read it.
+struct Uploader {
+    void* host[2] = {nullptr, nullptr};
+    size_t size[2] = {0, 0};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    int next = 0;
+
+    void release() {
+        for (int index = 0; index < 2; ++index) {
+            if (done[index] != nullptr) {
+                (void)hipEventSynchronize(done[index]);
+                (void)hipEventDestroy(done[index]);
+                done[index] = nullptr;
+            }
+            if (host[index] != nullptr) {
+                (void)hipHostFree(host[index]);
+                host[index] = nullptr;
+            }
+            size[index] = 0;
+        }
+    }
+
+    // Returns a pinned buffer of at least `bytes` that is safe to write now.
+    void* acquire(size_t bytes) {
+        const int index = next;
+        if (done[index] == nullptr) {
+            check_hip(hipEventCreateWithFlags(&done[index], hipEventDisableTiming), "upload event");
+        } else {
+            check_hip(hipEventSynchronize(done[index]), "upload wait");
+        }
+        if (size[index] < bytes) {
+            if (host[index] != nullptr) {
+                check_hip(hipHostFree(host[index]), "free staging");
+                host[index] = nullptr;
+            }
+            const size_t rounded = std::max<size_t>(bytes, 64 * 1024);
+            check_hip(hipHostMalloc(&host[index], rounded, hipHostMallocDefault), "staging buffer");
+            size[index] = rounded;
+        }
+        return host[index];
+    }
+
+    void copy(void* device, size_t bytes, hipStream_t stream) {
+        const int index = next;
+        check_hip(hipMemcpyAsync(device, host[index], bytes, hipMemcpyHostToDevice, stream), "upload");
+        check_hip(hipEventRecord(done[index], stream), "upload record");
+        next ^= 1;
+    }
+};
+
+struct Dims {
+    uint32_t layers;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t max_positions;
+    uint32_t growth;
+    uint32_t page_tokens;
+    uint32_t precision;
+    uint32_t slots;
+    uint32_t step_tokens;
+    uint32_t max_pages;
+    uint32_t pages_per_slot;
+    uint64_t page_bytes;
+};
+
+}  // namespace
+}  // namespace synapse_kv
+
+struct SynapseKvCache {
+    synapse_kv::Dims dims{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint32_t split_keys = 512;
+    uint32_t prefill_runs = 1;
+    uint32_t prefill_split_keys = 16384;
+
+    // Host shadow of the allocator (same rules as the table kernel).
+    std::vector<uint32_t> capacity;
+    std::vector<uint32_t> length;
+    std::vector<int32_t> table;  // [slots][pages_per_slot]
+    std::vector<int32_t> refcount;
+    std::vector<int32_t> free_stack;
+
+    // Device state.
+    uint8_t* pool = nullptr;
+    synapse_kv::DeviceBuffer<int32_t> block_table;
+    synapse_kv::DeviceBuffer<int32_t> device_refcount;
+    synapse_kv::DeviceBuffer<int32_t> device_free;
+    synapse_kv::DeviceBuffer<int32_t> device_state;
+    synapse_kv::DeviceBuffer<int32_t> fresh;
+    synapse_kv::DeviceBuffer<int32_t> copies;
+    synapse_kv::DeviceBuffer<float> cosines;
+    synapse_kv::DeviceBuffer<float> sines;
+    synapse_kv::DeviceBuffer<uint8_t> op_blob;  // table operations of the last call
+    synapse_kv::DeviceBuffer<uint8_t> blob;     // the step: tokens, decode items, merges, prefill items
+    synapse_kv::DeviceBuffer<float> partial_out;
+    synapse_kv::DeviceBuffer<float> partial_ml;
+    synapse_kv::Uploader uploader;
+
+    // Pending table operations of the current call and the list offsets they use.
+    std::vector<synapse_kv::TableOp> ops;
+    int32_t fresh_count = 0;
+    int32_t copy_count = 0;
+
+    // The current step.
+    bool step_ready = false;
+    int32_t step_count = 0;
+    int32_t decode_items = 0;
+    int32_t merge_items = 0;
+    int32_t prefill_items = 0;
+    size_t tokens_offset = 0;
+    size_t items_offset = 0;
+    size_t merges_offset = 0;
+    size_t prefill_offset = 0;
+
+    ~SynapseKvCache() {
+        (void)hipSetDevice(device);
+        (void)hipStreamSynchronize(stream);
+        uploader.release();
+        block_table.reset();
+        device_refcount.reset();
+        device_free.reset();
+        device_state.reset();
+        fresh.reset();
+        copies.reset();
+        cosines.reset();
+        sines.reset();
+        op_blob.reset();
+        blob.reset();
+        partial_out.reset();
+        partial_ml.reset();
+        if (pool != nullptr) {
+            (void)hipFree(pool);
+        }
+    }
+};
+
+namespace synapse_kv {
+namespace {
+
+uint32_t pages_for(const Dims& dims, uint32_t positions) { return (positions + dims.page_tokens - 1) / dims.page_tokens; }
+
+int32_t& slot_page(SynapseKvCache& cache, uint32_t slot, uint32_t logical) {
+    return cache.table[static_cast<size_t>(slot) * cache.dims.pages_per_slot + logical];
+}
+
+// Shadow resize (same order rules as table_kernel) and its table op.
+void shadow_resize(SynapseKvCache& cache, uint32_t slot, uint32_t positions) {
+    const uint32_t have = pages_for(cache.dims, cache.capacity[slot]);
+    const uint32_t want = pages_for(cache.dims, positions);
+    if (want != have) {
+        cache.ops.push_back(TableOp{kOpResize, static_cast<int32_t>(slot), static_cast<int32_t>(have),
+                                    static_cast<int32_t>(want), cache.fresh_count, {0, 0, 0}});
+    }
+    for (uint32_t page = have; page < want; ++page) {
+        const int32_t id = cache.free_stack.back();
+        cache.free_stack.pop_back();
+        cache.refcount[id] = 1;
+        slot_page(cache, slot, page) = id;
+        ++cache.fresh_count;
+    }
+    for (uint32_t page = have; page-- > want;) {
+        const int32_t id = slot_page(cache, slot, page);
+        if (--cache.refcount[id] == 0) {
+            cache.free_stack.push_back(id);
+        }
+        slot_page(cache, slot, page) = -1;
+    }
+    cache.capacity[slot] = positions;
+    cache.length[slot] = std::min(cache.length[slot], positions);
+}
+
+void check_slot(const SynapseKvCache& cache, uint32_t slot) {
+    if (slot >= cache.dims.slots) {
+        invalid("slot " + std::to_string(slot) + " is outside 0.." + std::to_string(cache.dims.slots - 1));
+    }
+}
+
+void set_device(const SynapseKvCache& cache) { check_hip(hipSetDevice(cache.device), "set device"); }
+
+// Sends the pending table ops and runs the table, zero-fill and copy kernels.
+void flush_ops(SynapseKvCache& cache) {
+    if (cache.ops.empty()) {
+        return;
+    }
+    const size_t bytes = cache.ops.size() * sizeof(TableOp);
+    cache.op_blob.ensure(bytes, "operation buffer");
+    void* staging = cache.uploader.acquire(bytes);
+    std::memcpy(staging, cache.ops.data(), bytes);
+    cache.uploader.copy(cache.op_blob.pointer, bytes, cache.stream);
+    TableArgs args{};
+    args.ops = reinterpret_cast<const TableOp*>(cache.op_blob.pointer);
+    args.op_count = static_cast<int32_t>(cache.ops.size());
+    args.pages_per_slot = static_cast<int32_t>(cache.dims.pages_per_slot);
+    args.max_pages = static_cast<int32_t>(cache.dims.max_pages);
+    args.block_table = cache.block_table.pointer;
+    args.refcount = cache.device_refcount.pointer;
+    args.free_stack = cache.device_free.pointer;
+    args.state = cache.device_state.pointer;
+    args.fresh = cache.fresh.pointer;
+    args.copies = cache.copies.pointer;
+    check_hip(launch_table(cache.stream, args), "table kernel");
+    PageArgs zero{cache.pool, cache.dims.page_bytes, cache.fresh.pointer, cache.fresh_count};
+    check_hip(launch_zero_pages(cache.stream, zero), "zero pages");
+    PageArgs copy{cache.pool, cache.dims.page_bytes, cache.copies.pointer, cache.copy_count};
+    check_hip(launch_copy_pages(cache.stream, copy), "copy pages");
+    cache.ops.clear();
+    cache.fresh_count = 0;
+    cache.copy_count = 0;
+}
+
+Geometry geometry(const SynapseKvCache& cache, uint32_t layer) {
+    Geometry g{};
+    g.pool = cache.pool;
+    g.page_bytes = cache.dims.page_bytes;
+    g.block_table = cache.block_table.pointer;
+    g.pages_per_slot = static_cast<int32_t>(cache.dims.pages_per_slot);
+    g.page_tokens = static_cast<int32_t>(cache.dims.page_tokens);
+    g.heads = static_cast<int32_t>(cache.dims.heads);
+    g.kv_heads = static_cast<int32_t>(cache.dims.kv_heads);
+    g.group = static_cast<int32_t>(cache.dims.heads / cache.dims.kv_heads);
+    g.head_dim = static_cast<int32_t>(cache.dims.head_dim);
+    g.layer = static_cast<int32_t>(layer);
+    return g;
+}
+
+size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1) / alignment * alignment; }
+
+void check_device_pointer(const void* pointer, const char* name) {
+    if (pointer == nullptr) {
+        fail(SYNAPSE_KV_NULL_POINTER, std::string("null pointer: ") + name);
+    }
+    hipPointerAttribute_t attributes{};
+    if (hipPointerGetAttributes(&attributes, pointer) != hipSuccess || attributes.type != hipMemoryTypeDevice) {
+        (void)hipGetLastError();
+        invalid(std::string(name) + " must be device memory");
+    }
+}
+
+// Builds and uploads the attention plan of a prepared step.
+void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t count) {
+    const Dims& dims = cache.dims;
+    std::vector<DecodeItem> items;
+    std::vector<MergeItem> merges;
+    std::vector<PrefillItem> prefill;
+    int32_t rows = 0;
+    const uint32_t split = cache.split_keys;
+    auto add_decode = [&](int32_t index) {
+        const int32_t keys = tokens[index].position + 1;
+        const int32_t splits = (keys + static_cast<int32_t>(split) - 1) / static_cast<int32_t>(split);
+        if (splits <= 1) {
+            for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
+                items.push_back(DecodeItem{index, static_cast<int32_t>(kv_head), 0, keys, -1, {0, 0, 0}});
+            }
+            return;
+        }
+        merges.push_back(MergeItem{index, rows, splits, 0});
+        for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
+            for (int32_t part = 0; part < splits; ++part) {
+                const int32_t begin = part * static_cast<int32_t>(split);
+                const int32_t end = std::min(keys, begin + static_cast<int32_t>(split));
+                items.push_back(DecodeItem{index, static_cast<int32_t>(kv_head), begin, end,
+                                           rows + static_cast<int32_t>(kv_head) * splits + part, {0, 0, 0}});
+            }
+        }
+        rows += splits * static_cast<int32_t>(dims.kv_heads);
+    };
+    // Prompt runs (plan_attention, schedule.rs:34-86): consecutive tokens of one slot at consecutive positions.
+    int32_t start = 0;
+    while (start < count) {
+        int32_t end = start + 1;
+        while (end < count && tokens[end].slot == tokens[start].slot &&
+               tokens[end].position == tokens[end - 1].position + 1) {
+            ++end;
+        }
+        if (end - start == 1 || cache.prefill_runs == 0 || dims.precision != SYNAPSE_KV_F16) {
+            for (int32_t index = start; index < end; ++index) {
+                add_decode(index);
+            }
+        } else {
+            for (int32_t first = start; first < end; first += kPrefillTokens) {
+                const int32_t size = std::min<int32_t>(kPrefillTokens, end - first);
+                const int32_t keys = tokens[first + size - 1].position + 1;
+                const int32_t chunk = static_cast<int32_t>(cache.prefill_split_keys);
+                const int32_t splits = (keys + chunk - 1) / chunk;
+                const int32_t stride = static_cast<int32_t>(dims.kv_heads) * splits;
+                if (splits > 1) {
+                    for (int32_t j = 0; j < size; ++j) {
+                        merges.push_back(MergeItem{first + j, rows + j * stride, splits, 0});
+                    }
+                }
+                for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
+                    for (int32_t part = 0; part < splits; ++part) {
+                        const int32_t begin = part * chunk;
+                        const int32_t finish = std::min(keys, begin + chunk);
+                        const int32_t row = splits > 1 ? rows + static_cast<int32_t>(kv_head) * splits + part : -1;
+                        prefill.push_back(PrefillItem{first, size, static_cast<int32_t>(kv_head), begin, finish, row,
+                                                      stride, 0});
+                    }
+                }
+                if (splits > 1) {
+                    rows += size * stride;
+                }
+            }
+        }
+        start = end;
+    }
+    const size_t tokens_bytes = static_cast<size_t>(count) * sizeof(SynapseKvBatchToken);
+    cache.tokens_offset = 0;
+    cache.items_offset = align_up(tokens_bytes, 256);
+    cache.merges_offset = align_up(cache.items_offset + items.size() * sizeof(DecodeItem), 256);
+    cache.prefill_offset = align_up(cache.merges_offset + merges.size() * sizeof(MergeItem), 256);
+    const size_t total = cache.prefill_offset + prefill.size() * sizeof(PrefillItem);
+    cache.blob.ensure(total, "step buffer");
+    const size_t group = dims.heads / dims.kv_heads;
+    cache.partial_out.ensure(static_cast<size_t>(rows) * group * dims.head_dim, "attention partials");
+    cache.partial_ml.ensure(static_cast<size_t>(rows) * group * 2, "attention partial statistics");
+    auto* staging = static_cast<uint8_t*>(cache.uploader.acquire(total));
+    std::memcpy(staging + cache.tokens_offset, tokens, tokens_bytes);
+    std::memcpy(staging + cache.items_offset, items.data(), items.size() * sizeof(DecodeItem));
+    std::memcpy(staging + cache.merges_offset, merges.data(), merges.size() * sizeof(MergeItem));
+    std::memcpy(staging + cache.prefill_offset, prefill.data(), prefill.size() * sizeof(PrefillItem));
+    cache.uploader.copy(cache.blob.pointer, total, cache.stream);
+    cache.step_count = count;
+    cache.decode_items = static_cast<int32_t>(items.size());
+    cache.merge_items = static_cast<int32_t>(merges.size());
+    cache.prefill_items = static_cast<int32_t>(prefill.size());
+    cache.step_ready = true;
+}
+
+void validate_desc(const SynapseKvDesc& desc) {
+    if (desc.rope_cosines == nullptr || desc.rope_sines == nullptr) {
+        fail(SYNAPSE_KV_NULL_POINTER, "null pointer: RoPE tables");
+    }
+    if (desc.layer_count == 0 || desc.heads == 0 || desc.kv_heads == 0 || desc.heads % desc.kv_heads != 0) {
+        invalid("layer, head and KV head counts must be positive, heads a multiple of KV heads");
+    }
+    if (desc.heads / desc.kv_heads > 8) {
+        invalid("at most 8 query heads per KV head (MAX_GROUP)");
+    }
+    if (desc.head_dim != 64 && desc.head_dim != 128) {
+        fail(SYNAPSE_KV_UNAVAILABLE, "unavailable: head dimension " + std::to_string(desc.head_dim) +
+                                         " (kernels exist for 64 and 128)");
+    }
+    if (desc.kv_precision != SYNAPSE_KV_F32 && desc.kv_precision != SYNAPSE_KV_F16) {
+        invalid("unknown KV precision " + std::to_string(desc.kv_precision));
+    }
+    if (desc.page_tokens < 64 || desc.page_tokens > 1024 || desc.page_tokens % 64 != 0) {
+        invalid("page_tokens must be a multiple of 64 in 64..1024");
+    }
+    if (desc.kv_growth_positions == 0 || desc.kv_growth_positions % desc.page_tokens != 0) {
+        invalid("kv_growth_positions must be a positive multiple of page_tokens");
+    }
+    if (desc.max_positions == 0 || desc.session_slots == 0 || desc.step_tokens == 0 || desc.max_pages == 0) {
+        invalid("max_positions, session_slots, step_tokens and max_pages must be positive");
+    }
+    if (desc.max_positions > (1u << 30) || desc.max_pages > (1u << 30) || desc.session_slots > (1u << 16)) {
+        invalid("max_positions, max_pages or session_slots is too large");
+    }
+}
+
+void create_cache(const SynapseKvDesc& desc, SynapseKvCache** output) {
+    validate_desc(desc);
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
+        (void)hipGetLastError();
+        fail(SYNAPSE_KV_UNAVAILABLE, "unavailable: no HIP device");
+    }
+    if (desc.device < 0 || desc.device >= devices) {
+        invalid("device " + std::to_string(desc.device) + " does not exist");
+    }
+    auto* cache = new SynapseKvCache();
+    try {
+        Dims& dims = cache->dims;
+        dims.layers = desc.layer_count;
+        dims.heads = desc.heads;
+        dims.kv_heads = desc.kv_heads;
+        dims.head_dim = desc.head_dim;
+        dims.max_positions = desc.max_positions;
+        dims.growth = desc.kv_growth_positions;
+        dims.page_tokens = desc.page_tokens;
+        dims.precision = desc.kv_precision;
+        dims.slots = desc.session_slots;
+        dims.step_tokens = desc.step_tokens;
+        dims.max_pages = desc.max_pages;
+        dims.pages_per_slot = pages_for(dims, dims.max_positions);
+        dims.page_bytes = static_cast<uint64_t>(dims.layers) * 2 * dims.kv_heads * dims.page_tokens * dims.head_dim *
+                          (dims.precision == SYNAPSE_KV_F16 ? 2 : 4);
+        cache->device = desc.device;
+        set_device(*cache);
+        cache->capacity.assign(dims.slots, 0);
+        cache->length.assign(dims.slots, 0);
+        cache->table.assign(static_cast<size_t>(dims.slots) * dims.pages_per_slot, -1);
+        cache->refcount.assign(dims.max_pages, 0);
+        cache->free_stack.resize(dims.max_pages);
+        for (uint32_t index = 0; index < dims.max_pages; ++index) {
+            cache->free_stack[index] = static_cast<int32_t>(dims.max_pages - 1 - index);
+        }
+        check_hip(hipMalloc(reinterpret_cast<void**>(&cache->pool), dims.page_bytes * dims.max_pages), "page pool");
+        cache->block_table.ensure(cache->table.size(), "block table");
+        cache->device_refcount.ensure(dims.max_pages, "reference counts");
+        cache->device_free.ensure(dims.max_pages, "free stack");
+        cache->device_state.ensure(4, "allocator state");
+        cache->fresh.ensure(dims.max_pages, "fresh page list");
+        cache->copies.ensure(2ull * dims.max_pages, "copy list");
+        const size_t rope = static_cast<size_t>(dims.max_positions) * (dims.head_dim / 2);
+        cache->cosines.ensure(rope, "RoPE cosines");
+        cache->sines.ensure(rope, "RoPE sines");
+        check_hip(hipMemcpy(cache->block_table.pointer, cache->table.data(), cache->table.size() * 4,
+                            hipMemcpyHostToDevice), "block table upload");
+        check_hip(hipMemcpy(cache->device_refcount.pointer, cache->refcount.data(), dims.max_pages * 4ull,
+                            hipMemcpyHostToDevice), "reference count upload");
+        check_hip(hipMemcpy(cache->device_free.pointer, cache->free_stack.data(), dims.max_pages * 4ull,
+                            hipMemcpyHostToDevice), "free stack upload");
+        const int32_t state[4] = {static_cast<int32_t>(dims.max_pages), 0, 0, 0};
+        check_hip(hipMemcpy(cache->device_state.pointer, state, sizeof(state), hipMemcpyHostToDevice), "state upload");
+        check_hip(hipMemcpy(cache->cosines.pointer, desc.rope_cosines, rope * 4, hipMemcpyHostToDevice), "RoPE upload");
+        check_hip(hipMemcpy(cache->sines.pointer, desc.rope_sines, rope * 4, hipMemcpyHostToDevice), "RoPE upload");
+    } catch (...) {
+        delete cache;
+        throw;
+    }
+    *output = cache;
+}
+
+// Growth and copy-on-write of a step in the restatement's order; throws before mutating on any failure.
+void prepare_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t count) {
+    const Dims& dims = cache.dims;
+    std::vector<uint32_t> needed(dims.slots, 0);
+    for (int32_t index = 0; index < count; ++index) {
+        const SynapseKvBatchToken& token = tokens[index];
+        if (token.slot < 0 || static_cast<uint32_t>(token.slot) >= dims.slots || token.position < 0 ||
+            static_cast<uint32_t>(token.position) >= dims.max_positions) {
+            invalid("batch token " + std::to_string(index) + " (slot " + std::to_string(token.slot) + ", position " +
+                    std::to_string(token.position) + ") is out of range");
+        }
+        needed[token.slot] = std::max<uint32_t>(needed[token.slot], static_cast<uint32_t>(token.position) + 1);
+    }
+    std::vector<uint32_t> grown(dims.slots);
+    size_t pops = 0;
+    for (uint32_t slot = 0; slot < dims.slots; ++slot) {
+        grown[slot] = cache.capacity[slot];
+        if (needed[slot] > cache.capacity[slot]) {
+            grown[slot] = next_capacity(needed[slot], cache.capacity[slot], dims.growth, dims.max_positions);
+            pops += pages_for(dims, grown[slot]) - pages_for(dims, cache.capacity[slot]);
+        }
+    }
+    {
+        std::vector<int32_t> references;
+        std::vector<std::pair<uint32_t, uint32_t>> owned;
+        for (int32_t index = 0; index < count; ++index) {
+            const uint32_t slot = static_cast<uint32_t>(tokens[index].slot);
+            const uint32_t page = static_cast<uint32_t>(tokens[index].position) / dims.page_tokens;
+            if (page >= pages_for(dims, cache.capacity[slot])) {
+                continue;
+            }
+            const int32_t id = slot_page(cache, slot, page);
+            if (cache.refcount[id] <= 1) {
+                continue;
+            }
+            if (references.empty()) {
+                references = cache.refcount;
+            }
+            const auto key = std::make_pair(slot, page);
+            if (std::find(owned.begin(), owned.end(), key) == owned.end() && references[id] > 1) {
+                --references[id];
+                ++pops;
+                owned.push_back(key);
+            }
+        }
+    }
+    if (pops > cache.free_stack.size()) {
+        fail(SYNAPSE_KV_OUT_OF_MEMORY, "out of device memory: the step needs " + std::to_string(pops) +
+                                           " pages and " + std::to_string(cache.free_stack.size()) + " are free");
+    }
+    for (uint32_t slot = 0; slot < dims.slots; ++slot) {
+        if (grown[slot] != cache.capacity[slot]) {
+            shadow_resize(cache, slot, grown[slot]);
+        }
+    }
+    for (int32_t index = 0; index < count; ++index) {
+        const uint32_t slot = static_cast<uint32_t>(tokens[index].slot);
+        const uint32_t page = static_cast<uint32_t>(tokens[index].position) / dims.page_tokens;
+        int32_t& entry = slot_page(cache, slot, page);
+        if (cache.refcount[entry] > 1) {
+            const int32_t fresh = cache.free_stack.back();
+            cache.free_stack.pop_back();
+            cache.refcount[fresh] = 1;
+            --cache.refcount[entry];
+            entry = fresh;
+            cache.ops.push_back(TableOp{kOpCow, static_cast<int32_t>(slot), static_cast<int32_t>(page),
+                                        cache.copy_count, 0, {0, 0, 0}});
+            ++cache.copy_count;
+        }
+    }
+    for (uint32_t slot = 0; slot < dims.slots; ++slot) {
+        cache.length[slot] = std::max(cache.length[slot], needed[slot]);
+    }
+}
+
+void require_step(const SynapseKvCache& cache, uint32_t layer) {
+    if (!cache.step_ready) {
+        invalid("no prepared step: call synapse_kv_step first");
+    }
+    if (layer >= cache.dims.layers) {
+        invalid("layer " + std::to_string(layer) + " is outside 0.." + std::to_string(cache.dims.layers - 1));
+    }
+}
+
+}  // namespace
+}  // namespace synapse_kv
+
+using namespace synapse_kv;
+
+extern "C" {
+
+uint32_t synapse_kv_abi_version(void) { return SYNAPSE_KV_ABI_VERSION; }
+
+int32_t synapse_kv_probe(SynapseKvDeviceInfo* info) {
+    if (info == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: device info");
+    }
+    return guarded([&] {
+        int devices = 0;
+        if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
+            (void)hipGetLastError();
+            fail(SYNAPSE_KV_UNAVAILABLE, "unavailable: no HIP device");
+        }
+        int device = 0;
+        check_hip(hipGetDevice(&device), "current device");
+        hipDeviceProp_t properties{};
+        check_hip(hipGetDeviceProperties(&properties, device), "device properties");
+        SynapseKvDeviceInfo described{};
+        std::string name = properties.name;
+        if (std::strlen(properties.gcnArchName) != 0) {
+            name += std::string(" (") + properties.gcnArchName + ")";
+        }
+        std::memcpy(described.name, name.data(), std::min<size_t>(name.size(), sizeof(described.name) - 1));
+        described.recommended_working_set_bytes = properties.totalGlobalMem;
+        described.max_buffer_bytes = properties.totalGlobalMem;
+        described.unified_memory = properties.integrated ? 1 : 0;
+        described.apple_family = 0;
+        *info = described;
+    });
+}
+
+size_t synapse_kv_last_error(uint8_t* buffer, size_t capacity) {
+    const std::string& message = g_last_error;
+    if (buffer != nullptr) {
+        std::memcpy(buffer, message.data(), std::min(capacity, message.size()));
+    }
+    return message.size();
+}
+
+int32_t synapse_kv_cache_create(const SynapseKvDesc* desc, SynapseKvCache** cache) {
+    if (desc == nullptr || cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache description or output");
+    }
+    return guarded([&] { create_cache(*desc, cache); });
+}
+
+void synapse_kv_cache_destroy(SynapseKvCache* cache) { delete cache; }
+
+int32_t synapse_kv_set_stream(SynapseKvCache* cache, void* stream) {
+    if (cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache");
+    }
+    return guarded([&] {
+        set_device(*cache);
+        check_hip(hipStreamSynchronize(cache->stream), "stream switch");
+        cache->stream = static_cast<hipStream_t>(stream);
+    });
+}
+
+int32_t synapse_kv_set_option(SynapseKvCache* cache, uint32_t option, uint32_t value) {
+    if (cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache");
+    }
+    return guarded([&] {
+        if (option == SYNAPSE_KV_OPTION_SPLIT_KEYS) {
+            if (value == 0 || value % kStepKeys != 0) {
+                invalid("split keys must be a positive multiple of 64");
+            }
+            cache->split_keys = value;
+        } else if (option == SYNAPSE_KV_OPTION_PREFILL_RUNS) {
+            cache->prefill_runs = value != 0 ? 1 : 0;
+        } else if (option == SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS) {
+            if (value == 0 || value % kStepKeys != 0) {
+                invalid("prefill split keys must be a positive multiple of 64");
+            }
+            cache->prefill_split_keys = value;
+        } else {
+            invalid("unknown option " + std::to_string(option));
+        }
+        cache->step_ready = false;
+    });
+}
+
+uint64_t synapse_kv_bytes(const SynapseKvCache* cache) {
+    if (cache == nullptr) {
+        return 0;
+    }
+    const uint64_t used = cache->dims.max_pages - cache->free_stack.size();
+    return used * cache->dims.page_bytes;
+}
+
+int32_t synapse_kv_reserve(SynapseKvCache* cache, uint32_t slot, uint32_t positions) {
+    if (cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache");
+    }
+    return guarded([&] {
+        check_slot(*cache, slot);
+        const Dims& dims = cache->dims;
+        if (positions > dims.max_positions) {
+            invalid("reserve needs at most the context positions (" + std::to_string(dims.max_positions) + ")");
+        }
+        const uint32_t current = cache->capacity[slot];
+        const uint32_t rounded = reserve_rounded(positions, dims.growth, dims.max_positions);
+        if (positions > current || (rounded < current && rounded <= current / 4)) {
+            const uint32_t need = pages_for(dims, rounded) > pages_for(dims, current)
+                                      ? pages_for(dims, rounded) - pages_for(dims, current)
+                                      : 0;
+            if (need > cache->free_stack.size()) {
+                fail(SYNAPSE_KV_OUT_OF_MEMORY, "out of device memory: reserve needs " + std::to_string(need) +
+                                                   " pages and " + std::to_string(cache->free_stack.size()) +
+                                                   " are free");
+            }
+            set_device(*cache);
+            shadow_resize(*cache, slot, rounded);
+            flush_ops(*cache);
+        }
+    });
+}
+
+int32_t synapse_kv_release(SynapseKvCache* cache, uint32_t slot) {
+    if (cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache");
+    }
+    return guarded([&] {
+        check_slot(*cache, slot);
+        set_device(*cache);
+        shadow_resize(*cache, slot, 0);
+        cache->length[slot] = 0;
+        flush_ops(*cache);
+    });
+}
+
+int32_t synapse_kv_truncate(SynapseKvCache* cache, uint32_t slot, uint32_t length) {
+    if (cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache");
+    }
+    return guarded([&] {
+        check_slot(*cache, slot);
+        if (length > cache->length[slot]) {
+            invalid("truncate target " + std::to_string(length) + " is beyond the written length " +
+                    std::to_string(cache->length[slot]));
+        }
+        cache->length[slot] = length;
+    });
+}
+
+int32_t synapse_kv_fork(SynapseKvCache* cache, uint32_t source, uint32_t target) {
+    if (cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache");
+    }
+    return guarded([&] {
+        check_slot(*cache, source);
+        check_slot(*cache, target);
+        if (source == target || cache->capacity[target] != 0) {
+            invalid("fork needs a different, empty target slot");
+        }
+        const Dims& dims = cache->dims;
+        const uint32_t shared = pages_for(dims, cache->length[source]);
+        for (uint32_t page = 0; page < shared; ++page) {
+            const int32_t id = slot_page(*cache, source, page);
+            slot_page(*cache, target, page) = id;
+            ++cache->refcount[id];
+        }
+        cache->capacity[target] = std::min(dims.max_positions, shared * dims.page_tokens);
+        cache->length[target] = cache->length[source];
+        if (shared != 0) {
+            set_device(*cache);
+            cache->ops.push_back(TableOp{kOpFork, static_cast<int32_t>(source), static_cast<int32_t>(target),
+                                         static_cast<int32_t>(shared), 0, {0, 0, 0}});
+            flush_ops(*cache);
+        }
+    });
+}
+
+int32_t synapse_kv_step(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count) {
+    if (cache == nullptr || tokens == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or tokens");
+    }
+    return guarded([&] {
+        if (count == 0 || count > cache->dims.step_tokens) {
+            invalid("a step holds 1.." + std::to_string(cache->dims.step_tokens) + " tokens");
+        }
+        set_device(*cache);
+        cache->step_ready = false;
+        prepare_step(*cache, tokens, static_cast<int32_t>(count));
+        flush_ops(*cache);
+        plan_step(*cache, tokens, static_cast<int32_t>(count));
+    });
+}
+
+int32_t synapse_kv_append_rope(SynapseKvCache* cache, uint32_t layer, float* qkv, uint32_t qkv_stride) {
+    if (cache == nullptr || qkv == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or qkv");
+    }
+    return guarded([&] {
+        require_step(*cache, layer);
+        const Dims& dims = cache->dims;
+        if (qkv_stride < (dims.heads + 2 * dims.kv_heads) * dims.head_dim) {
+            invalid("qkv_stride is shorter than (heads + 2 * kv_heads) * head_dim");
+        }
+        set_device(*cache);
+        check_device_pointer(qkv, "qkv");
+        AppendArgs args{};
+        args.geo = geometry(*cache, layer);
+        args.pool = cache->pool;
+        args.tokens = reinterpret_cast<const SynapseKvBatchToken*>(cache->blob.pointer + cache->tokens_offset);
+        args.qkv = qkv;
+        args.qkv_stride = static_cast<int32_t>(qkv_stride);
+        args.half_dim = static_cast<int32_t>(dims.head_dim / 2);
+        args.cosines = cache->cosines.pointer;
+        args.sines = cache->sines.pointer;
+        check_hip(launch_append(cache->stream, args, cache->step_count, dims.precision == SYNAPSE_KV_F16), "append");
+    });
+}
+
+int32_t synapse_kv_attention(SynapseKvCache* cache, uint32_t layer, const float* qkv, uint32_t qkv_stride,
+                             float* output, uint32_t out_stride) {
+    if (cache == nullptr || qkv == nullptr || output == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache, qkv or output");
+    }
+    return guarded([&] {
+        require_step(*cache, layer);
+        const Dims& dims = cache->dims;
+        if (qkv_stride < dims.heads * dims.head_dim || qkv_stride % 4 != 0) {
+            invalid("qkv_stride must be a multiple of 4 and hold heads * head_dim query values");
+        }
+        if (out_stride < dims.heads * dims.head_dim) {
+            invalid("out_stride is shorter than heads * head_dim");
+        }
+        if (reinterpret_cast<uintptr_t>(qkv) % 16 != 0) {
+            invalid("qkv must be 16-byte aligned");
+        }
+        set_device(*cache);
+        check_device_pointer(qkv, "qkv");
+        check_device_pointer(output, "output");
+        AttentionArgs args{};
+        args.geo = geometry(*cache, layer);
+        args.tokens = reinterpret_cast<const SynapseKvBatchToken*>(cache->blob.pointer + cache->tokens_offset);
+        args.qkv = qkv;
+        args.qkv_stride = static_cast<int32_t>(qkv_stride);
+        args.output = output;
+        args.out_stride = static_cast<int32_t>(out_stride);
+        args.scale_log2 = 1.4426950408889634f / std::sqrt(static_cast<float>(dims.head_dim));
+        args.items = reinterpret_cast<const DecodeItem*>(cache->blob.pointer + cache->items_offset);
+        args.merges = reinterpret_cast<const MergeItem*>(cache->blob.pointer + cache->merges_offset);
+        args.prefill = reinterpret_cast<const PrefillItem*>(cache->blob.pointer + cache->prefill_offset);
+        args.partial_out = cache->partial_out.pointer;
+        args.partial_ml = cache->partial_ml.pointer;
+        const bool fp16 = dims.precision == SYNAPSE_KV_F16;
+        check_hip(launch_prefill(cache->stream, args, cache->prefill_items, fp16), "prefill attention");
+        check_hip(launch_decode(cache->stream, args, cache->decode_items, fp16), "decode attention");
+        check_hip(launch_merge(cache->stream, args, cache->merge_items), "split merge");
+    });
+}
+
+int32_t synapse_kv_synchronize(SynapseKvCache* cache) {
+    if (cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache");
+    }
+    return guarded([&] {
+        set_device(*cache);
+        check_hip(hipStreamSynchronize(cache->stream), "synchronize");
+    });
+}
+
+int32_t synapse_kv_slot_info(const SynapseKvCache* cache, uint32_t slot, uint32_t* capacity, uint32_t* length,
+                             uint32_t* pages) {
+    if (cache == nullptr || capacity == nullptr || length == nullptr || pages == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or output");
+    }
+    return guarded([&] {
+        check_slot(*cache, slot);
+        *capacity = cache->capacity[slot];
+        *length = cache->length[slot];
+        *pages = pages_for(cache->dims, cache->capacity[slot]);
+    });
+}
+
+int32_t synapse_kv_read_block_table(SynapseKvCache* cache, uint32_t slot, int32_t* pages, size_t capacity,
+                                    size_t* count) {
+    if (cache == nullptr || pages == nullptr || count == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or output");
+    }
+    return guarded([&] {
+        check_slot(*cache, slot);
+        const size_t entries = cache->dims.pages_per_slot;
+        if (capacity < entries) {
+            invalid("the output holds fewer entries than pages_per_slot (" + std::to_string(entries) + ")");
+        }
+        set_device(*cache);
+        check_hip(hipStreamSynchronize(cache->stream), "synchronize");
+        check_hip(hipMemcpy(pages, cache->block_table.pointer + static_cast<size_t>(slot) * entries, entries * 4,
+                            hipMemcpyDeviceToHost), "block table read");
+        *count = entries;
+    });
+}
+
+int32_t synapse_kv_read_refcounts(SynapseKvCache* cache, int32_t* counts, size_t capacity) {
+    if (cache == nullptr || counts == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or output");
+    }
+    return guarded([&] {
+        if (capacity < cache->dims.max_pages) {
+            invalid("the output holds fewer entries than max_pages");
+        }
+        set_device(*cache);
+        check_hip(hipStreamSynchronize(cache->stream), "synchronize");
+        check_hip(hipMemcpy(counts, cache->device_refcount.pointer, cache->dims.max_pages * 4ull, hipMemcpyDeviceToHost),
+                  "reference count read");
+    });
+}
+
+int32_t synapse_kv_read_free_list(SynapseKvCache* cache, int32_t* pages, size_t capacity, size_t* count) {
+    if (cache == nullptr || pages == nullptr || count == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or output");
+    }
+    return guarded([&] {
+        set_device(*cache);
+        check_hip(hipStreamSynchronize(cache->stream), "synchronize");
+        int32_t state[4] = {0, 0, 0, 0};
+        check_hip(hipMemcpy(state, cache->device_state.pointer, sizeof(state), hipMemcpyDeviceToHost), "state read");
+        const size_t entries = static_cast<size_t>(std::max(0, state[0]));
+        if (capacity < entries) {
+            invalid("the output holds fewer entries than the free stack");
+        }
+        check_hip(hipMemcpy(pages, cache->device_free.pointer, entries * 4, hipMemcpyDeviceToHost), "free stack read");
+        *count = entries;
+    });
+}
+
+int32_t synapse_kv_page_stats(SynapseKvCache* cache, SynapseKvPageStats* stats) {
+    if (cache == nullptr || stats == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or output");
+    }
+    return guarded([&] {
+        set_device(*cache);
+        check_hip(hipStreamSynchronize(cache->stream), "synchronize");
+        int32_t state[4] = {0, 0, 0, 0};
+        check_hip(hipMemcpy(state, cache->device_state.pointer, sizeof(state), hipMemcpyDeviceToHost), "state read");
+        SynapseKvPageStats out{};
+        out.max_pages = cache->dims.max_pages;
+        out.free_pages = static_cast<uint32_t>(cache->free_stack.size());
+        out.used_pages = out.max_pages - out.free_pages;
+        for (int32_t count : cache->refcount) {
+            out.shared_pages += count > 1 ? 1 : 0;
+        }
+        out.page_bytes = cache->dims.page_bytes;
+        out.kv_bytes = static_cast<uint64_t>(out.used_pages) * out.page_bytes;
+        out.device_status = static_cast<uint32_t>(state[1]);
+        if (state[0] != static_cast<int32_t>(out.free_pages) && out.device_status == 0) {
+            out.device_status = 3;  // device free count differs from the host shadow
+        }
+        *stats = out;
+    });
+}
+
+int32_t synapse_kv_read_kv(SynapseKvCache* cache, uint32_t slot, uint32_t layer, uint32_t first, uint32_t count,
+                           void* keys, void* values) {
+    if (cache == nullptr || keys == nullptr || values == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or output");
+    }
+    return guarded([&] {
+        check_slot(*cache, slot);
+        const Dims& dims = cache->dims;
+        if (layer >= dims.layers) {
+            invalid("layer out of range");
+        }
+        if (static_cast<uint64_t>(first) + count > cache->capacity[slot]) {
+            invalid("positions beyond the slot capacity");
+        }
+        if (count == 0) {
+            return;
+        }
+        set_device(*cache);
+        const size_t element = dims.precision == SYNAPSE_KV_F16 ? 2 : 4;
+        const size_t bytes = static_cast<size_t>(count) * dims.kv_heads * dims.head_dim * element;
+        DeviceBuffer<uint8_t> staging;
+        staging.ensure(2 * bytes, "read staging");
+        GatherArgs args{};
+        args.geo = geometry(*cache, layer);
+        args.slot = static_cast<int32_t>(slot);
+        args.first = static_cast<int32_t>(first);
+        args.count = static_cast<int32_t>(count);
+        args.keys = staging.pointer;
+        args.values = staging.pointer + bytes;
+        hipError_t error = launch_gather(cache->stream, args, dims.precision == SYNAPSE_KV_F16);
+        if (error == hipSuccess) {
+            error = hipStreamSynchronize(cache->stream);
+        }
+        if (error == hipSuccess) {
+            error = hipMemcpy(keys, staging.pointer, bytes, hipMemcpyDeviceToHost);
+        }
+        if (error == hipSuccess) {
+            error = hipMemcpy(values, staging.pointer + bytes, bytes, hipMemcpyDeviceToHost);
+        }
+        staging.reset();
+        check_hip(error, "KV read");
+    });
+}
+
+int32_t synapse_kv_rope_table(uint32_t head_dim, float theta, float yarn_factor, uint32_t yarn_original,
+                              uint32_t positions, float* cosines, float* sines) {
+    if (cosines == nullptr || sines == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: RoPE tables");
+    }
+    return guarded([&] {
+        if (head_dim == 0 || (head_dim & 1u) != 0 || !std::isfinite(theta) || theta <= 1.0f) {
+            invalid("RoPE needs an even head dimension and theta above one");
+        }
+        // RopeFrequencies (RopeFrequencies.cs:20-81), FP32 expression order as written there.
+        const uint32_t half = head_dim / 2;
+        const float pi = 3.14159265358979323846f;
+        std::vector<float> mix;
+        float magnitude = 1.0f;
+        if (yarn_factor > 0.0f) {
+            if (yarn_original == 0) {
+                invalid("YaRN needs the original context length");
+            }
+            magnitude = 1.0f + (0.1f * std::log(yarn_factor));
+            auto correction = [&](float rotations) {
+                return static_cast<float>(head_dim) *
+                       std::log(static_cast<float>(yarn_original) / (rotations * 2 * pi)) / (2 * std::log(theta));
+            };
+            const float low = std::max(0.0f, std::floor(correction(32.0f)));
+            const float high = std::min(static_cast<float>(head_dim - 1), std::ceil(correction(1.0f)));
+            mix.resize(half);
+            for (uint32_t index = 0; index < half; ++index) {
+                const float ramp = (static_cast<float>(index) - low) / std::max(0.001f, high - low);
+                mix[index] = 1 - std::min(1.0f, std::max(0.0f, ramp));
+            }
+        }
+        for (uint32_t position = 0; position < positions; ++position) {
+            for (uint32_t index = 0; index < half; ++index) {
+                const float exponent = 2.0f * static_cast<float>(index) / static_cast<float>(head_dim);
+                const float angle = static_cast<float>(position) / std::pow(theta, exponent);
+                const size_t at = static_cast<size_t>(position) * half + index;
+                if (mix.empty()) {
+                    cosines[at] = std::cos(angle);
+                    sines[at] = std::sin(angle);
+                } else {
+                    const float scaled = (angle / yarn_factor * (1 - mix[index])) + (angle * mix[index]);
+                    cosines[at] = std::cos(scaled) * magnitude;
+                    sines[at] = std::sin(scaled) * magnitude;
+                }
+            }
+        }
+    });
+}
+
+}  // extern "C"

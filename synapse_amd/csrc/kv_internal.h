@@ -1,0 +1,155 @@
+// Internal interface between the host half of libsynapse_kv (cache.hip) and its kernels.
+//
+// Page layout (one page = page_tokens positions of one slot across every executed layer):
+//   region(layer, which, kv_head) = ((layer * 2 + which) * kv_heads + kv_head) * page_tokens * head_dim elements
+//   which = 0 (K): row-major [page_tokens][head_dim]   -- a 16-byte load holds 8 dims of one key
+//   which = 1 (V): transposed [head_dim][page_tokens]  -- a 16-byte load holds 8 keys of one dim
+// so both MFMA products of attention (S^T = K Q^T and O^T = V^T P^T) read their A operand straight from HBM
+// with 128-bit loads. Elements are float (FP32 KV) or _Float16 (FP16 KV).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/synapse_kv.h"
+
+namespace synapse_kv {
+
+// A block-table operation, executed in order by the single-workgroup table kernel.
+enum TableOpKind : int32_t {
+    kOpResize = 1,  // slot, from pages, to pages, list offset (fresh pages on growth)
+    kOpCow = 2,     // slot, logical page, list offset (copy pair)
+    kOpFork = 3,    // source slot, target slot, pages
+};
+
+struct TableOp {
+    int32_t kind;
+    int32_t a;
+    int32_t b;
+    int32_t c;
+    int32_t d;
+    int32_t pad[3];
+};
+static_assert(sizeof(TableOp) == 32, "TableOp is 32 bytes");
+
+struct TableArgs {
+    const TableOp* ops;
+    int32_t op_count;
+    int32_t pages_per_slot;
+    int32_t max_pages;
+    int32_t* block_table;  // [slots][pages_per_slot]
+    int32_t* refcount;     // [max_pages]
+    int32_t* free_stack;   // [max_pages], bottom first
+    int32_t* state;        // [0] free count, [1] status (0 = consistent)
+    int32_t* fresh;        // pages to zero-fill
+    int32_t* copies;       // (source, target) page pairs to copy
+};
+
+struct PageArgs {
+    uint8_t* pool;
+    uint64_t page_bytes;
+    const int32_t* list;  // fresh pages, or (source, target) pairs
+    int32_t count;
+};
+
+// One decode split-K work item: keys [key_begin, key_end) of one token's slot for one KV head. `row` >= 0 is the
+// partial row of a split token; -1 writes the normalized output directly.
+struct DecodeItem {
+    int32_t token;
+    int32_t kv_head;
+    int32_t key_begin;
+    int32_t key_end;
+    int32_t row;
+    int32_t pad[3];
+};
+static_assert(sizeof(DecodeItem) == 32, "DecodeItem is 32 bytes");
+
+// A split token for the merge: its first partial row and its split count (rows = first + kv_head * splits + s).
+struct MergeItem {
+    int32_t token;
+    int32_t first_row;
+    int32_t splits;
+    int32_t pad;
+};
+
+// A prefill work item: `count` (<= kPrefillTokens) consecutive tokens of one prompt run (consecutive positions of
+// one slot) starting at step token `first_token`, every query head of `kv_head`, keys [key_begin, key_end).
+// `row` >= 0: token j of the item writes partial row `row + j * row_stride` (the decode merge layout);
+// -1: the normalized output is written directly.
+struct PrefillItem {
+    int32_t first_token;
+    int32_t count;
+    int32_t kv_head;
+    int32_t key_begin;
+    int32_t key_end;
+    int32_t row;
+    int32_t row_stride;
+    int32_t pad;
+};
+static_assert(sizeof(PrefillItem) == 32, "PrefillItem is 32 bytes");
+
+struct Geometry {
+    const uint8_t* pool;
+    uint64_t page_bytes;
+    const int32_t* block_table;
+    int32_t pages_per_slot;
+    int32_t page_tokens;
+    int32_t heads;
+    int32_t kv_heads;
+    int32_t group;
+    int32_t head_dim;
+    int32_t layer;
+};
+
+struct AppendArgs {
+    Geometry geo;
+    uint8_t* pool;
+    const SynapseKvBatchToken* tokens;
+    float* qkv;
+    int32_t qkv_stride;
+    int32_t half_dim;
+    const float* cosines;
+    const float* sines;
+};
+
+struct AttentionArgs {
+    Geometry geo;
+    const SynapseKvBatchToken* tokens;
+    const float* qkv;
+    int32_t qkv_stride;
+    float* output;
+    int32_t out_stride;
+    float scale_log2;  // log2(e) / sqrt(head_dim)
+    const DecodeItem* items;
+    const MergeItem* merges;
+    const PrefillItem* prefill;
+    float* partial_out;  // [rows][group][head_dim]
+    float* partial_ml;   // [rows][group][2] (maximum in log2 units, sum)
+};
+
+struct GatherArgs {
+    Geometry geo;
+    int32_t slot;
+    int32_t first;
+    int32_t count;
+    uint8_t* keys;    // [count][kv_heads][head_dim] in the storage type
+    uint8_t* values;  // [count][kv_heads][head_dim] in the storage type
+};
+
+// Launchers (each enqueues on `stream` and returns the launch status).
+hipError_t launch_table(hipStream_t stream, const TableArgs& args);
+hipError_t launch_zero_pages(hipStream_t stream, const PageArgs& args);
+hipError_t launch_copy_pages(hipStream_t stream, const PageArgs& args);
+hipError_t launch_append(hipStream_t stream, const AppendArgs& args, int tokens, bool fp16);
+hipError_t launch_decode(hipStream_t stream, const AttentionArgs& args, int items, bool fp16);
+hipError_t launch_merge(hipStream_t stream, const AttentionArgs& args, int merges);
+hipError_t launch_prefill(hipStream_t stream, const AttentionArgs& args, int items, bool fp16);
+hipError_t launch_gather(hipStream_t stream, const GatherArgs& args, bool fp16);
+
+// Query rows (tokens) per prefill work item: 16 per MFMA column tile, kPrefillTiles tiles per wave.
+constexpr int kPrefillTiles = 2;
+constexpr int kPrefillTokens = 16 * kPrefillTiles;
+// Keys per decode/prefill inner step.
+constexpr int kStepKeys = 64;
+
+}  // namespace synapse_kv

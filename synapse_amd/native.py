@@ -1,0 +1,217 @@
+"""ctypes binding of libsynapse_kv, mirroring Synapse's managed loader.
+
+The conventions follow ``NativeGpuLibrary`` (src/Synapse.Runtime/Features/GpuKernels/NativeGpuLibrary.cs):
+the library is loaded from an explicit path, its ABI version is checked before any other call
+(``NativeGpuLibrary.cs:49-75``), and failing status codes become exceptions with the library's
+thread-local message (``ThrowIfFailed``): status 3 -> :class:`NotSupportedError`
+(NotSupportedException), 5 -> :class:`InsufficientMemoryError` (InsufficientMemoryException), anything
+else -> :class:`InvalidOperationError` (InvalidOperationException).
+
+There is no fallback: a missing or mismatched library raises :class:`NotSupportedError`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+ABI_VERSION = 1
+LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libsynapse_kv.so"
+
+STATUS_OK = 0
+STATUS_NULL_POINTER = 1
+STATUS_INVALID_ARGUMENT = 2
+STATUS_UNAVAILABLE = 3
+STATUS_DEVICE_ERROR = 4
+STATUS_OUT_OF_MEMORY = 5
+STATUS_PANIC = 6
+
+KV_F32 = 0
+KV_F16 = 1
+
+OPTION_SPLIT_KEYS = 1
+OPTION_PREFILL_RUNS = 2
+OPTION_PREFILL_SPLIT_KEYS = 3
+
+
+class SynapseKvError(RuntimeError):
+    """A failing status from the library, with its status code and message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+class NotSupportedError(SynapseKvError):
+    """Status 3: the library, device or requested shape is unavailable."""
+
+
+class InsufficientMemoryError(SynapseKvError, MemoryError):
+    """Status 5: a device allocation failed or the page pool is exhausted."""
+
+
+class InvalidOperationError(SynapseKvError):
+    """Any other failing status (null pointer, invalid argument, device error, caught exception)."""
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_uint8 * 128),
+        ("recommended_working_set_bytes", ctypes.c_uint64),
+        ("max_buffer_bytes", ctypes.c_uint64),
+        ("unified_memory", ctypes.c_uint32),
+        ("apple_family", ctypes.c_uint32),
+    ]
+
+
+class BatchToken(ctypes.Structure):
+    """BatchToken (native/synapse-gpu/src/Features/GpuKernels/decoder.rs:133-141)."""
+
+    _fields_ = [
+        ("slot", ctypes.c_int32),
+        ("token", ctypes.c_int32),
+        ("position", ctypes.c_int32),
+        ("logits_row", ctypes.c_int32),
+    ]
+
+
+class CacheDesc(ctypes.Structure):
+    _fields_ = [
+        ("rope_cosines", ctypes.POINTER(ctypes.c_float)),
+        ("rope_sines", ctypes.POINTER(ctypes.c_float)),
+        ("layer_count", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32),
+        ("kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("max_positions", ctypes.c_uint32),
+        ("kv_growth_positions", ctypes.c_uint32),
+        ("page_tokens", ctypes.c_uint32),
+        ("kv_precision", ctypes.c_uint32),
+        ("session_slots", ctypes.c_uint32),
+        ("step_tokens", ctypes.c_uint32),
+        ("max_pages", ctypes.c_uint32),
+        ("device", ctypes.c_int32),
+    ]
+
+
+class PageStats(ctypes.Structure):
+    _fields_ = [
+        ("max_pages", ctypes.c_uint32),
+        ("free_pages", ctypes.c_uint32),
+        ("used_pages", ctypes.c_uint32),
+        ("shared_pages", ctypes.c_uint32),
+        ("page_bytes", ctypes.c_uint64),
+        ("kv_bytes", ctypes.c_uint64),
+        ("device_status", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+# Sizes pinned on both sides of the ABI (include/synapse_kv.h static assertions).
+STRUCT_SIZES = {DeviceInfo: 152, BatchToken: 16, CacheDesc: 64, PageStats: 40}
+for _struct, _size in STRUCT_SIZES.items():
+    assert ctypes.sizeof(_struct) == _size, (_struct.__name__, ctypes.sizeof(_struct))
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+_SIZE = ctypes.c_size_t
+
+# name -> (restype, argtypes); the complete exported surface of include/synapse_kv.h.
+EXPORTS = {
+    "synapse_kv_abi_version": (_U32, []),
+    "synapse_kv_probe": (_I32, [ctypes.POINTER(DeviceInfo)]),
+    "synapse_kv_last_error": (_SIZE, [ctypes.c_char_p, _SIZE]),
+    "synapse_kv_cache_create": (_I32, [ctypes.POINTER(CacheDesc), ctypes.POINTER(_P)]),
+    "synapse_kv_cache_destroy": (None, [_P]),
+    "synapse_kv_set_stream": (_I32, [_P, _P]),
+    "synapse_kv_set_option": (_I32, [_P, _U32, _U32]),
+    "synapse_kv_bytes": (_U64, [_P]),
+    "synapse_kv_reserve": (_I32, [_P, _U32, _U32]),
+    "synapse_kv_release": (_I32, [_P, _U32]),
+    "synapse_kv_truncate": (_I32, [_P, _U32, _U32]),
+    "synapse_kv_fork": (_I32, [_P, _U32, _U32]),
+    "synapse_kv_step": (_I32, [_P, ctypes.POINTER(BatchToken), _SIZE]),
+    "synapse_kv_append_rope": (_I32, [_P, _U32, _P, _U32]),
+    "synapse_kv_attention": (_I32, [_P, _U32, _P, _U32, _P, _U32]),
+    "synapse_kv_synchronize": (_I32, [_P]),
+    "synapse_kv_slot_info": (
+        _I32,
+        [_P, _U32, ctypes.POINTER(_U32), ctypes.POINTER(_U32), ctypes.POINTER(_U32)],
+    ),
+    "synapse_kv_read_block_table": (_I32, [_P, _U32, _P, _SIZE, ctypes.POINTER(_SIZE)]),
+    "synapse_kv_read_refcounts": (_I32, [_P, _P, _SIZE]),
+    "synapse_kv_read_free_list": (_I32, [_P, _P, _SIZE, ctypes.POINTER(_SIZE)]),
+    "synapse_kv_page_stats": (_I32, [_P, ctypes.POINTER(PageStats)]),
+    "synapse_kv_read_kv": (_I32, [_P, _U32, _U32, _U32, _U32, _P, _P]),
+    "synapse_kv_rope_table": (_I32, [_U32, ctypes.c_float, ctypes.c_float, _U32, _U32, _P, _P]),
+}
+
+
+class NativeKvLibrary:
+    """The loaded library with typed entry points and status checking."""
+
+    _lock = threading.Lock()
+    _loaded: "NativeKvLibrary | None" = None
+
+    def __init__(self, path: Path):
+        self.path = Path(path)
+        if not self.path.exists():
+            raise NotSupportedError(STATUS_UNAVAILABLE, f"{self.path}: the library file is missing; build it first")
+        try:
+            self.handle = ctypes.CDLL(str(self.path))
+        except OSError as error:
+            raise NotSupportedError(STATUS_UNAVAILABLE, f"{self.path}: the loader could not load it: {error}")
+        version_function = self.handle.synapse_kv_abi_version
+        version_function.restype = _U32
+        version_function.argtypes = []
+        version = version_function()
+        if version != ABI_VERSION:
+            raise NotSupportedError(
+                STATUS_UNAVAILABLE, f"{self.path}: its ABI version {version} differs from the required {ABI_VERSION}"
+            )
+        for name, (restype, argtypes) in EXPORTS.items():
+            function = getattr(self.handle, name)
+            function.restype = restype
+            function.argtypes = argtypes
+            setattr(self, "c_" + name[len("synapse_kv_"):], function)
+
+    @classmethod
+    def load(cls, path: Path | None = None) -> "NativeKvLibrary":
+        with cls._lock:
+            if path is not None:
+                return cls(path)
+            if cls._loaded is None:
+                cls._loaded = cls(LIBRARY_PATH)
+            return cls._loaded
+
+    def last_error(self) -> str:
+        """NativeGpuLibrary.LastError: query the length, then copy the message out."""
+        length = self.c_last_error(None, 0)
+        buffer = ctypes.create_string_buffer(max(1, length))
+        self.c_last_error(buffer, length)
+        return buffer.raw[:length].decode("utf-8", "replace")
+
+    def check(self, status: int) -> None:
+        """ThrowIfFailed: maps a failing status to the matching exception."""
+        if status == STATUS_OK:
+            return
+        message = self.last_error()
+        if status == STATUS_UNAVAILABLE:
+            raise NotSupportedError(status, message)
+        if status == STATUS_OUT_OF_MEMORY:
+            raise InsufficientMemoryError(status, message)
+        raise InvalidOperationError(status, message)
+
+    def probe(self) -> dict:
+        info = DeviceInfo()
+        self.check(self.c_probe(ctypes.byref(info)))
+        raw = bytes(info.name)
+        return {
+            "name": raw.split(b"\0", 1)[0].decode("utf-8", "replace"),
+            "recommended_working_set_bytes": info.recommended_working_set_bytes,
+            "max_buffer_bytes": info.max_buffer_bytes,
+            "unified_memory": bool(info.unified_memory),
+        }

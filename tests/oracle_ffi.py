@@ -1,0 +1,276 @@
+"""ctypes access to the CPU restatement in oracle/ (test infrastructure only)."""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_PATH = ROOT / "oracle" / "build" / "liboracle.so"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+SIGNATURES = {
+    "orc_f32_to_f16": (None, [_P, _P, ctypes.c_size_t]),
+    "orc_f16_to_f32": (None, [_P, _P, ctypes.c_size_t]),
+    "orc_rope_table": (_I, [_I, _F, _F, _I, _I, _P, _P]),
+    "orc_rope_apply": (None, [_P, _I, _I, _P, _P]),
+    "orc_next_capacity": (_I, [_I, _I, _I, _I]),
+    "orc_dense_create": (_P, [_I, _I, _I, _I]),
+    "orc_dense_destroy": (None, [_P]),
+    "orc_dense_store": (_I, [_P, _I, _I, _P, _P, _I]),
+    "orc_dense_reserve": (_I, [_P, _I]),
+    "orc_dense_release": (None, [_P]),
+    "orc_dense_allocated": (_I, [_P]),
+    "orc_dense_bytes": (ctypes.c_longlong, [_P]),
+    "orc_dense_get": (_I, [_P, _I, _I, _I, _I, _I, _P]),
+    "orc_paged_create": (_P, [_I] * 11),
+    "orc_paged_destroy": (None, [_P]),
+    "orc_paged_reserve": (_I, [_P, _I, _I]),
+    "orc_paged_release": (_I, [_P, _I]),
+    "orc_paged_truncate": (_I, [_P, _I, _I]),
+    "orc_paged_fork": (_I, [_P, _I, _I]),
+    "orc_paged_step": (_I, [_P, _P, _I]),
+    "orc_paged_append_rope": (_I, [_P, _I, _P, _I, _P, _P]),
+    "orc_paged_gather": (_I, [_P, _I, _I, _I, _I, _P, _P, _I]),
+    "orc_paged_slot": (_I, [_P, _I, _P, _P, _P]),
+    "orc_paged_table": (_I, [_P, _I, _P]),
+    "orc_paged_refcounts": (None, [_P, _P]),
+    "orc_paged_free_list": (_I, [_P, _P]),
+    "orc_paged_kv_bytes": (ctypes.c_longlong, [_P]),
+    "orc_attention_scalar": (None, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "orc_attention_managed": (None, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "orc_attention_fp64": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
+    "orc_attention_split": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "orc_paged_attention": (ctypes.c_double, [_P, _I, _P, _I, _P, _I, _I]),
+    "orc_plan_attention": (_I, [_P, _I, _I, _I, _P, _I, _P]),
+    "orc_prefix_create": (_P, [_I]),
+    "orc_prefix_destroy": (None, [_P]),
+    "orc_prefix_claim": (_I, [_P, _P, _I]),
+    "orc_prefix_remember": (None, [_P, _P, _I, _P, _I]),
+    "orc_prefix_clear": (None, [_P]),
+}
+
+
+def load() -> ctypes.CDLL:
+    if not ORACLE_PATH.exists():
+        subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+    library = ctypes.CDLL(str(ORACLE_PATH))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        function = getattr(library, name)
+        function.restype = restype
+        function.argtypes = argtypes
+    return library
+
+
+ORACLE = load()
+
+
+def ptr(array: np.ndarray) -> int:
+    assert array.flags["C_CONTIGUOUS"]
+    return array.ctypes.data
+
+
+def f32_to_f16(values) -> np.ndarray:
+    source = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(source.shape, dtype=np.uint16)
+    ORACLE.orc_f32_to_f16(ptr(source), ptr(out), source.size)
+    return out
+
+
+def f16_to_f32(bits) -> np.ndarray:
+    source = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(source.shape, dtype=np.float32)
+    ORACLE.orc_f16_to_f32(ptr(source), ptr(out), source.size)
+    return out
+
+
+def rope_table(head_dim, theta, positions, yarn_factor=0.0, yarn_original=0):
+    half = head_dim // 2
+    cos = np.empty((positions, half), dtype=np.float32)
+    sin = np.empty((positions, half), dtype=np.float32)
+    status = ORACLE.orc_rope_table(head_dim, theta, yarn_factor, yarn_original, positions, ptr(cos), ptr(sin))
+    assert status == 0, status
+    return cos, sin
+
+
+def rope_apply(values, heads, head_dim, cos_row, sin_row) -> np.ndarray:
+    out = np.ascontiguousarray(values, dtype=np.float32).copy()
+    c = np.ascontiguousarray(cos_row, dtype=np.float32)
+    s = np.ascontiguousarray(sin_row, dtype=np.float32)
+    ORACLE.orc_rope_apply(ptr(out), heads, head_dim, ptr(c), ptr(s))
+    return out
+
+
+def attention(kind, query, keys, values, heads, kv_heads, head_dim, position, split_keys=None):
+    """Attention of one query position over dense [positions][kv_heads][head_dim] K/V (fp32)."""
+    q = np.ascontiguousarray(query, dtype=np.float32)
+    k = np.ascontiguousarray(keys, dtype=np.float32)
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.zeros(heads * head_dim, dtype=np.float32)
+    if kind == "scalar":
+        ORACLE.orc_attention_scalar(ptr(q), ptr(k), ptr(v), heads, kv_heads, head_dim, position, ptr(out))
+    elif kind == "managed":
+        ORACLE.orc_attention_managed(ptr(q), ptr(k), ptr(v), heads, kv_heads, head_dim, position, ptr(out))
+    elif kind == "split":
+        ORACLE.orc_attention_split(ptr(q), ptr(k), ptr(v), heads, kv_heads, head_dim, position, split_keys, ptr(out))
+    elif kind == "fp64":
+        scale = np.float32(1.0) / np.sqrt(np.float32(head_dim))
+        status = ORACLE.orc_attention_fp64(ptr(q), ptr(k), ptr(v), None, heads, kv_heads, head_dim, position,
+                                           float(scale), ptr(out))
+        assert status == 0, status
+    else:
+        raise ValueError(kind)
+    return out
+
+
+class DenseCache:
+    """Qwen2KvCache restatement."""
+
+    def __init__(self, layers, maximum, kv_width, growth):
+        self.handle = ORACLE.orc_dense_create(layers, maximum, kv_width, growth)
+        assert self.handle
+        self.kv_width = kv_width
+
+    def __del__(self):
+        ORACLE.orc_dense_destroy(self.handle)
+
+    def store(self, layer, position, key, value):
+        k = np.ascontiguousarray(key, dtype=np.float32)
+        v = np.ascontiguousarray(value, dtype=np.float32)
+        return ORACLE.orc_dense_store(self.handle, layer, position, ptr(k), ptr(v), k.size)
+
+    def reserve(self, positions):
+        return ORACLE.orc_dense_reserve(self.handle, positions)
+
+    def release(self):
+        ORACLE.orc_dense_release(self.handle)
+
+    @property
+    def allocated(self):
+        return ORACLE.orc_dense_allocated(self.handle)
+
+    @property
+    def allocated_bytes(self):
+        return ORACLE.orc_dense_bytes(self.handle)
+
+    def get(self, layer, position, head, head_dim, value=False):
+        out = np.empty(head_dim, dtype=np.float32)
+        status = ORACLE.orc_dense_get(self.handle, layer, position, head, head_dim, 1 if value else 0, ptr(out))
+        return status, out
+
+
+class PagedCache:
+    """The paged restatement (the specification the GPU table kernels follow)."""
+
+    def __init__(self, layers, heads, kv_heads, head_dim, maximum, growth, page_tokens, precision, slots,
+                 max_pages, step_tokens):
+        self.handle = ORACLE.orc_paged_create(layers, heads, kv_heads, head_dim, maximum, growth, page_tokens,
+                                              precision, slots, max_pages, step_tokens)
+        assert self.handle
+        self.heads, self.kv_heads, self.head_dim = heads, kv_heads, head_dim
+        self.precision = precision
+        self.max_pages = max_pages
+        self.pages_per_slot = -(-maximum // page_tokens)
+
+    def __del__(self):
+        ORACLE.orc_paged_destroy(self.handle)
+
+    def reserve(self, slot, positions):
+        return ORACLE.orc_paged_reserve(self.handle, slot, positions)
+
+    def release(self, slot):
+        return ORACLE.orc_paged_release(self.handle, slot)
+
+    def truncate(self, slot, length):
+        return ORACLE.orc_paged_truncate(self.handle, slot, length)
+
+    def fork(self, source, target):
+        return ORACLE.orc_paged_fork(self.handle, source, target)
+
+    def step(self, tokens):
+        array = np.ascontiguousarray(tokens, dtype=np.int32)
+        if array.shape[1] == 2:
+            full = np.zeros((array.shape[0], 4), dtype=np.int32)
+            full[:, 0], full[:, 2], full[:, 3] = array[:, 0], array[:, 1], -1
+            array = full
+        return ORACLE.orc_paged_step(self.handle, ptr(array), array.shape[0])
+
+    def append_rope(self, layer, qkv, cos, sin):
+        assert qkv.dtype == np.float32 and qkv.flags["C_CONTIGUOUS"]
+        return ORACLE.orc_paged_append_rope(self.handle, layer, ptr(qkv), qkv.shape[1], ptr(cos), ptr(sin))
+
+    def gather(self, slot, layer, first, count, raw=False):
+        dtype = np.uint16 if (raw and self.precision == 1) else np.float32
+        k = np.zeros((count, self.kv_heads, self.head_dim), dtype=dtype)
+        v = np.zeros_like(k)
+        status = ORACLE.orc_paged_gather(self.handle, slot, layer, first, count, ptr(k), ptr(v), 1 if raw else 0)
+        assert status == 0, status
+        return k, v
+
+    def slot(self, slot):
+        cap, length, pages = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        status = ORACLE.orc_paged_slot(self.handle, slot, ctypes.byref(cap), ctypes.byref(length),
+                                       ctypes.byref(pages))
+        assert status == 0
+        return {"capacity": cap.value, "length": length.value, "pages": pages.value}
+
+    def table(self, slot):
+        out = np.empty(self.pages_per_slot, dtype=np.int32)
+        assert ORACLE.orc_paged_table(self.handle, slot, ptr(out)) == 0
+        return out
+
+    def refcounts(self):
+        out = np.empty(self.max_pages, dtype=np.int32)
+        ORACLE.orc_paged_refcounts(self.handle, ptr(out))
+        return out
+
+    def free_list(self):
+        out = np.empty(self.max_pages, dtype=np.int32)
+        count = ORACLE.orc_paged_free_list(self.handle, ptr(out))
+        return out[:count]
+
+    @property
+    def kv_bytes(self):
+        return ORACLE.orc_paged_kv_bytes(self.handle)
+
+    def attention(self, layer, qkv, out, threads=1):
+        return ORACLE.orc_paged_attention(self.handle, layer, ptr(qkv), qkv.shape[1], ptr(out), out.shape[1],
+                                          threads)
+
+
+def plan_attention(tokens, kv_heads, run_tokens):
+    array = np.ascontiguousarray(tokens, dtype=np.int32)
+    capacity = max(1, array.shape[0] * kv_heads)
+    blocks = np.zeros((capacity, 8), dtype=np.uint32)
+    summary = np.zeros(4, dtype=np.uint32)
+    count = ORACLE.orc_plan_attention(ptr(array), array.shape[0], kv_heads, run_tokens, ptr(blocks), capacity,
+                                      ptr(summary))
+    assert count >= 0
+    return blocks[:count], {"run_blocks": int(summary[0]), "single_blocks": int(summary[1]),
+                            "split_keys": int(summary[2]), "splits": int(summary[3])}
+
+
+class Prefix:
+    def __init__(self, enabled=True):
+        self.handle = ORACLE.orc_prefix_create(1 if enabled else 0)
+
+    def __del__(self):
+        ORACLE.orc_prefix_destroy(self.handle)
+
+    def claim(self, prompt):
+        array = np.ascontiguousarray(prompt, dtype=np.int32)
+        return ORACLE.orc_prefix_claim(self.handle, ptr(array), array.size)
+
+    def remember(self, prompt, generated):
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        g = np.ascontiguousarray(generated, dtype=np.int32)
+        ORACLE.orc_prefix_remember(self.handle, ptr(p), p.size, ptr(g), g.size)
+
+    def clear(self):
+        ORACLE.orc_prefix_clear(self.handle)

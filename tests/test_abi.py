@@ -1,0 +1,115 @@
+"""The C ABI without a GPU: every declared symbol is exported, struct sizes are pinned, and the error paths follow
+the reference's conventions (ffi.rs: status codes, thread-local last error, null-safe destroy and kv_bytes)."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle_ffi import rope_table as oracle_rope_table
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "synapse_kv.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(synapse_kv_\w+)\s*\(", text, flags=re.MULTILINE)))
+
+
+def test_every_declared_function_is_exported(native):
+    names = declared_functions()
+    assert len(names) >= 20
+    exported = subprocess.run(["nm", "-D", "--defined-only", str(native.path)], capture_output=True, text=True,
+                              check=True).stdout
+    symbols = set(re.findall(r"\b(synapse_kv_\w+)\b", exported))
+    assert set(names) == symbols, (set(names) ^ symbols)
+    from synapse_amd.native import EXPORTS
+    assert set(EXPORTS) == set(names)
+
+
+@pytest.mark.parametrize("compiler,flag", [("gcc", "-std=c11"), ("g++", "-std=c++17")])
+def test_header_compiles_with_pinned_sizes(compiler, flag, tmp_path):
+    source = tmp_path / ("probe.c" if compiler == "gcc" else "probe.cpp")
+    source.write_text('#include "synapse_kv.h"\nint main(void) { return (int)sizeof(SynapseKvDesc) - 64; }\n')
+    subprocess.run([compiler, flag, "-fsyntax-only", "-I", str(HEADER.parent), str(source)], check=True)
+
+
+def test_abi_version_and_struct_sizes(native):
+    from synapse_amd.native import ABI_VERSION, STRUCT_SIZES
+
+    assert native.c_abi_version() == ABI_VERSION == 1
+    for struct, size in STRUCT_SIZES.items():
+        assert ctypes.sizeof(struct) == size
+
+
+def test_status_codes_match_the_reference():
+    # error.rs:4-16.
+    from synapse_amd import native as n
+
+    assert [n.STATUS_OK, n.STATUS_NULL_POINTER, n.STATUS_INVALID_ARGUMENT, n.STATUS_UNAVAILABLE,
+            n.STATUS_DEVICE_ERROR, n.STATUS_OUT_OF_MEMORY, n.STATUS_PANIC] == list(range(7))
+
+
+def test_null_pointers_and_last_error_protocol(native):
+    assert native.c_probe(None) == 1
+    message = native.last_error()
+    assert "null pointer" in message
+    length = native.c_last_error(None, 0)
+    assert length == len(message.encode())
+    short = ctypes.create_string_buffer(4)
+    assert native.c_last_error(short, 4) == length
+    assert short.raw == message.encode()[:4]
+    assert native.c_cache_create(None, None) == 1
+    assert native.c_reserve(None, 0, 0) == 1
+    assert native.c_step(None, None, 0) == 1
+    assert native.c_attention(None, 0, None, 0, None, 0) == 1
+    assert native.c_bytes(None) == 0
+    native.c_cache_destroy(None)  # null is ignored
+
+
+def test_status_maps_to_the_managed_exceptions(native):
+    from synapse_amd.native import InsufficientMemoryError, InvalidOperationError, NotSupportedError
+
+    with pytest.raises(InvalidOperationError):
+        native.check(native.c_probe(None))
+    for status, kind in [(3, NotSupportedError), (5, InsufficientMemoryError), (2, InvalidOperationError),
+                         (4, InvalidOperationError), (6, InvalidOperationError)]:
+        with pytest.raises(kind):
+            native.check(status)
+
+
+def cpu_desc(**overrides):
+    from synapse_amd.native import CacheDesc
+
+    cos = np.zeros((64, 32), dtype=np.float32)
+    fields = dict(layer_count=2, heads=14, kv_heads=2, head_dim=64, max_positions=64, kv_growth_positions=64,
+                  page_tokens=64, kv_precision=1, session_slots=1, step_tokens=8, max_pages=2, device=0)
+    fields.update(overrides)
+    pointer = cos.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    return CacheDesc(pointer, pointer, *fields.values()), cos
+
+
+@pytest.mark.parametrize("overrides,status", [
+    ({"head_dim": 96}, 3), ({"kv_precision": 2}, 2), ({"heads": 15}, 2), ({"kv_growth_positions": 32}, 2),
+    ({"page_tokens": 100}, 2), ({"max_pages": 0}, 2), ({"heads": 18, "kv_heads": 2}, 2)])
+def test_create_validates_the_shape_before_the_device(native, overrides, status):
+    desc, _keep = cpu_desc(**overrides)
+    handle = ctypes.c_void_p()
+    assert native.c_cache_create(ctypes.byref(desc), ctypes.byref(handle)) == status
+    assert not handle.value
+
+
+def test_rope_table_entry_point_matches_the_restatement(native):
+    from synapse_amd import rope_table
+
+    for head_dim, factor, original in [(64, 0.0, 0), (128, 0.0, 0), (64, 4.0, 32768)]:
+        cos, sin = rope_table(head_dim, 1e6, 3000, factor, original, library=native)
+        ocos, osin = oracle_rope_table(head_dim, 1e6, 3000, factor, original)
+        assert np.array_equal(cos.view(np.uint32), ocos.view(np.uint32))
+        assert np.array_equal(sin.view(np.uint32), osin.view(np.uint32))
+    out = np.zeros(4, dtype=np.float32)
+    assert native.c_rope_table(63, 1e6, 0.0, 0, 1, out.ctypes.data, out.ctypes.data) == 2

@@ -1,0 +1,242 @@
+"""GPU parity through the C ABI: the HIP path against the CPU restatement on the same seeded inputs.
+
+Bar: block tables, reference counts, free stacks, rotated Q/K and stored K/V bits are bit-exact; attention is
+within |gpu - ref| <= 2e-3 + 1e-3 * |ref| of the FP32-accumulate restatement (Qwen2CpuAttention order).
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+from oracle_ffi import PagedCache
+from paged_checks import check_allocator_invariants
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+RTOL = 1e-3
+
+
+def say(*parts):
+    print(*parts, flush=True)
+    sys.stdout.flush()
+
+
+class Pair:
+    """A GPU cache and its CPU restatement driven with identical calls."""
+
+    def __init__(self, torch, *, layers=2, heads=14, kv_heads=2, head_dim=64, max_positions=4096, growth=256,
+                 page=256, precision="f16", slots=4, max_pages=64, step_tokens=256):
+        from synapse_amd import PagedKvCache
+
+        self.torch = torch
+        self.gpu = PagedKvCache(layers=layers, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
+                                max_positions=max_positions, growth_positions=growth, page_tokens=page,
+                                precision=precision, session_slots=slots, step_tokens=step_tokens,
+                                max_pages=max_pages)
+        code = 1 if precision == "f16" else 0
+        self.cpu = PagedCache(layers, heads, kv_heads, head_dim, max_positions, growth, page, code, slots,
+                              max_pages, step_tokens)
+        self.layers, self.heads, self.kv_heads, self.head_dim = layers, heads, kv_heads, head_dim
+        self.slots, self.max_pages = slots, max_pages
+        self.width = (heads + 2 * kv_heads) * head_dim
+        self.cos, self.sin = self.gpu.rope_cosines, self.gpu.rope_sines
+
+    def call(self, name, *args):
+        """Runs one table operation on both sides; both must succeed or fail alike."""
+        from synapse_amd import SynapseKvError
+
+        expected = getattr(self.cpu, name)(*args)
+        try:
+            getattr(self.gpu, name)(*args)
+            status = 0
+        except SynapseKvError as error:
+            status = error.status
+        assert status == expected, (name, args, status, expected)
+        return status
+
+    def step(self, tokens, rng, attend=True):
+        """One step: prepare, then per layer append (+ attention); checks every output."""
+        torch = self.torch
+        status = self.call("step", tokens)
+        if status:
+            return status
+        count = len(tokens)
+        for layer in range(self.layers):
+            rows = rng.standard_normal((count, self.width)).astype(np.float32)
+            qkv = torch.from_numpy(rows.copy()).cuda()
+            self.gpu.append_rope(layer, qkv)
+            assert self.cpu.append_rope(layer, rows, self.cos, self.sin) == 0
+            rotated = qkv.cpu().numpy()
+            assert np.array_equal(rotated.view(np.uint32), rows.view(np.uint32)), "rotated Q/K differ"
+            if attend:
+                out = torch.full((count, self.heads * self.head_dim), float("nan"), device="cuda")
+                self.gpu.attention(layer, qkv, out)
+                expected = np.zeros((count, self.heads * self.head_dim), dtype=np.float32)
+                self.cpu.attention(layer, rows, expected)
+                got = out.cpu().numpy()
+                error = np.abs(got - expected)
+                bound = ATOL + RTOL * np.abs(expected)
+                assert np.all(error <= bound), (layer, float(error.max()), tokens[:4])
+        return 0
+
+    def check_tables(self):
+        tables = []
+        for slot in range(self.slots):
+            gpu_table = self.gpu.block_table(slot)
+            assert np.array_equal(gpu_table, self.cpu.table(slot)), slot
+            assert self.gpu.slot_info(slot) == self.cpu.slot(slot)
+            tables.append(gpu_table)
+        refcounts = self.gpu.refcounts()
+        assert np.array_equal(refcounts, self.cpu.refcounts())
+        free = self.gpu.free_list()
+        assert np.array_equal(free, self.cpu.free_list())
+        check_allocator_invariants(tables, refcounts, free, self.max_pages)
+        stats = self.gpu.page_stats()
+        assert stats["device_status"] == 0
+        assert self.gpu.allocated_bytes == self.cpu.kv_bytes
+
+    def check_contents(self, slot):
+        capacity = self.cpu.slot(slot)["capacity"]
+        if capacity == 0:
+            return
+        for layer in range(self.layers):
+            keys, values = self.gpu.read_kv(slot, layer, 0, capacity)
+            ckeys, cvalues = self.cpu.gather(slot, layer, 0, capacity, raw=True)
+            assert np.array_equal(keys.view(np.uint8), ckeys.view(np.uint8)), (slot, layer)
+            assert np.array_equal(values.view(np.uint8), cvalues.view(np.uint8)), (slot, layer)
+
+
+SHAPES = [
+    # (heads, kv_heads, head_dim, precision, page)
+    (14, 2, 64, "f16", 256),
+    (28, 4, 128, "f16", 256),
+    (14, 2, 64, "f32", 64),
+    (28, 4, 128, "f32", 128),
+    (8, 8, 128, "f16", 64),
+]
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,precision,page", SHAPES)
+def test_decode_steps_match_the_restatement(torch_gpu, heads, kv_heads, head_dim, precision, page):
+    say("decode parity", heads, kv_heads, head_dim, precision, page)
+    pair = Pair(torch_gpu, heads=heads, kv_heads=kv_heads, head_dim=head_dim, precision=precision, page=page,
+                growth=max(page, 256), max_pages=96 if page == 64 else 48)
+    rng = np.random.default_rng(heads * 1000 + head_dim)
+    # Prefill three slots with ragged lengths through decode-only steps of many tokens (no prompt runs).
+    pair.gpu.set_prefill_runs(False)
+    lengths = [1, 300, 777]
+    for slot, length in enumerate(lengths):
+        for first in range(0, length, 200):
+            positions = range(first, min(length, first + 200))
+            assert pair.step([(slot, p) for p in positions], rng, attend=False) == 0
+    pair.check_tables()
+    for slot in range(3):
+        pair.check_contents(slot)
+    # Decode: one token per slot per step, unsplit and with many small splits.
+    for split in (512, 64, 128):
+        pair.gpu.set_split_keys(split)
+        tokens = [(slot, lengths[slot]) for slot in range(3)]
+        assert pair.step(tokens, rng) == 0
+        lengths = [length + 1 for length in lengths]
+    pair.check_tables()
+
+
+def test_single_position_and_page_boundaries(torch_gpu):
+    say("page boundaries")
+    pair = Pair(torch_gpu, page=64, growth=64, max_pages=64, heads=28, kv_heads=4, head_dim=128)
+    rng = np.random.default_rng(5)
+    for position in [0, 1, 63, 64, 65, 127, 128, 191, 255, 256]:
+        assert pair.step([(0, position)], rng) == 0
+    pair.gpu.set_split_keys(64)
+    assert pair.step([(0, 257)], rng) == 0
+    pair.check_tables()
+    pair.check_contents(0)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_prompt_runs_match_the_restatement(torch_gpu, head_dim):
+    say("prefill parity", head_dim)
+    heads, kv_heads = (14, 2) if head_dim == 64 else (28, 4)
+    pair = Pair(torch_gpu, heads=heads, kv_heads=kv_heads, head_dim=head_dim, max_pages=64)
+    rng = np.random.default_rng(head_dim)
+    # A first chunk, a second chunk that attends over the cache, and runs of two slots in one step.
+    assert pair.step([(0, p) for p in range(0, 100)], rng) == 0
+    assert pair.step([(0, p) for p in range(100, 233)], rng) == 0
+    pair.gpu.set_prefill_split_keys(64)
+    assert pair.step([(0, p) for p in range(233, 300)] + [(1, p) for p in range(0, 45)], rng) == 0
+    pair.gpu.set_prefill_split_keys(16384)
+    assert pair.step([(1, 45), (0, 300)] + [(2, p) for p in range(0, 31)], rng) == 0
+    pair.check_tables()
+    for slot in range(3):
+        pair.check_contents(slot)
+
+
+def test_table_operations_match_the_restatement(torch_gpu):
+    say("table operations")
+    pair = Pair(torch_gpu, page=64, growth=128, max_positions=1024, slots=5, max_pages=40, layers=1)
+    rng = np.random.default_rng(17)
+    lengths = [0] * 5
+    for round_index in range(60):
+        action = rng.random()
+        slot = int(rng.integers(0, 5))
+        if action < 0.45:
+            position = int(min(1023, lengths[slot] + rng.integers(0, 100)))
+            if pair.step([(slot, position)], rng, attend=False) == 0:
+                lengths[slot] = max(lengths[slot], position + 1)
+        elif action < 0.65:
+            pair.call("reserve", slot, int(rng.integers(0, 1025)))
+            lengths[slot] = min(lengths[slot], pair.cpu.slot(slot)["capacity"])
+        elif action < 0.8:
+            target = int(rng.integers(0, 5))
+            pair.call("fork", slot, target)
+            lengths[target] = pair.cpu.slot(target)["length"]
+        elif action < 0.9:
+            pair.call("release", slot)
+            lengths[slot] = 0
+        else:
+            pair.call("truncate", slot, int(rng.integers(0, lengths[slot] + 2)))
+            lengths[slot] = pair.cpu.slot(slot)["length"]
+        pair.check_tables()
+    for slot in range(5):
+        pair.check_contents(slot)
+
+
+def test_copy_on_write_keeps_both_histories(torch_gpu):
+    say("copy on write")
+    pair = Pair(torch_gpu, page=64, growth=64, max_positions=1024, slots=4, max_pages=48, heads=28, kv_heads=4,
+                head_dim=128)
+    rng = np.random.default_rng(23)
+    assert pair.step([(0, p) for p in range(150)], rng, attend=False) == 0
+    for target in (1, 2, 3):
+        pair.call("fork", 0, target)
+    # Every fork writes its own suffix into the shared partial page, then all decode together.
+    assert pair.step([(1, 150), (2, 150), (3, 150)], rng) == 0
+    assert pair.step([(0, 150), (1, 151), (2, 151), (3, 151)], rng) == 0
+    pair.check_tables()
+    for slot in range(4):
+        pair.check_contents(slot)
+
+
+def test_errors_follow_the_reference_mapping(torch_gpu):
+    from synapse_amd import InsufficientMemoryError, InvalidOperationError
+
+    say("error mapping")
+    pair = Pair(torch_gpu, page=64, growth=64, max_positions=512, slots=2, max_pages=4, layers=1)
+    with pytest.raises(InvalidOperationError):
+        pair.gpu.attention(0, torch_gpu.zeros(1, pair.width, device="cuda"),
+                           torch_gpu.zeros(1, pair.heads * pair.head_dim, device="cuda"))
+    with pytest.raises(InsufficientMemoryError):
+        pair.gpu.reserve(0, 512)
+    with pytest.raises(InvalidOperationError):
+        pair.gpu.reserve(0, 513)
+    with pytest.raises(InvalidOperationError):
+        pair.gpu.step([(2, 0)])
+    pair.gpu.step([(0, 0)])
+    host = np.zeros((1, pair.width), dtype=np.float32)
+    with pytest.raises(InvalidOperationError):
+        pair.gpu.append_rope(0, host.ctypes.data)  # host memory is rejected
+    with pytest.raises(InvalidOperationError):
+        pair.gpu.append_rope(1, torch_gpu.zeros(1, pair.width, device="cuda"))
+    assert pair.gpu.allocated_bytes == pair.gpu.page_stats()["page_bytes"]
