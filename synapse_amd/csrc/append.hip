@@ -10,6 +10,9 @@
 
 #include "kv_internal.h"
 
+// hipcc contracts a*b - c*d into a fused multiply-add by default; the rotation must round every product.
+#pragma clang fp contract(off)
+
 namespace synapse_kv {
 namespace {
 
@@ -52,8 +55,8 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         const float y = values[i + half];
         const float c = cosines[i];
         const float s = sines[i];
-        const float first = __fsub_rn(__fmul_rn(x, c), __fmul_rn(y, s));
-        const float second = __fadd_rn(__fmul_rn(x, s), __fmul_rn(y, c));
+        const float first = x * c - y * s;   // contraction is off for this file: two products, one difference
+        const float second = x * s + y * c;
         values[i] = first;
         values[i + half] = second;
         if (head >= g.heads) {
