@@ -40,7 +40,7 @@ extern "C" {
 #define SYNAPSE_KV_F16 1u
 
 /* Tuning options for synapse_kv_set_option. */
-#define SYNAPSE_KV_OPTION_SPLIT_KEYS 1u     /* keys per decode split-K work item; a multiple of 64 (default 512) */
+#define SYNAPSE_KV_OPTION_SPLIT_KEYS 1u     /* fewest keys per decode wave worker; a multiple of 64 (default 256) */
 #define SYNAPSE_KV_OPTION_PREFILL_RUNS 2u   /* 1: FP16 prompt runs use the MFMA prefill kernel (default); 0: decode path */
 #define SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS 3u /* keys per prefill split-K work item; a multiple of 64 (default 16384) */
 

@@ -1,21 +1,25 @@
-// GQA flash-decode attention with split-K over pages and a cross-split merge.
+// GQA flash-decode attention: persistent wave workers over an evenly split key space, then a split merge.
 //
 // Semantics: synapse_attention_decode (native/synapse-gpu/src/Features/GpuKernels/metal/shaders/
-// attention.metal:319-355) and synapse_attention_reduce (attention_reduce.metal:5-40): each work item attends one
-// token's query heads of one KV head (the GQA group) over keys [key_begin, key_end) of its slot with an online
-// softmax; a token whose keys span several items writes unnormalized output plus (max, sum) rows that the merge
-// kernel rescales by exp(m - max) and divides. Scores are q.k / sqrt(head_dim) over keys 0..position inclusive
-// (Qwen2Attention.cs:5-25).
+// attention.metal:319-355) and synapse_attention_reduce (attention_reduce.metal:5-40): the query heads of one KV
+// head (the GQA group) of one token attend keys 0..position of the token's slot (Qwen2Attention.cs:5-25) with an
+// online softmax; a key range split across workers leaves unnormalized output plus (max, sum) per head, and the
+// merge takes the max over splits with a positive sum, rescales by exp(m - max) and divides.
 //
-// MI355X mapping: one workgroup = 4 waves = one work item; each wave takes every fourth 64-key step. Per step a
-// wave computes S^T = K Q^T and O^T = V^T P^T on MFMA with the group's query heads as the 16 columns (7 of 16
-// used under GQA 7:1), so every K and V byte is read from HBM once per item and shared by all query heads:
+// Work split (MI355X): the host flattens every (token, KV head) row into 64-key steps and gives each resident wave
+// an equal contiguous share of the steps (about the same bytes per wave whatever the ragged lengths). A wave walks
+// its segments in order; a row that lies inside one wave is written normalized, a row cut by worker boundaries
+// writes partial rows that the merge kernel combines. No tail of idle CUs, and each wave reads every K/V byte of
+// its share once for all query heads of the group.
+//
+// Per 64-key step a wave computes S^T = K Q^T and O^T = V^T P^T on MFMA with the group's query heads as the 16
+// columns (7 of 16 used under GQA 7:1):
 //   FP16 KV: v_mfma_f32_16x16x32_f16. The A operand is 8 consecutive halves of one row: 8 dims of one key
-//            (K, row-major) or 8 keys of one dim (V, stored transposed), i.e. one 128-bit load per lane.
-//            The keys of the QK^T tiles are permuted so that the C layout of S^T (lane holds rows 4g..4g+3 of
-//            two tiles) is exactly the B layout of P^T for the PV product: no shuffle between the two MFMAs.
+//            (K, row-major) or 8 keys of one dim (V, stored transposed), one 128-bit load per lane. The keys of
+//            the QK^T tiles are permuted so the C layout of S^T (lane holds rows 4g..4g+3 of two tiles) is exactly
+//            the B layout of P^T for the PV product: no data movement between the two MFMAs.
 //   FP32 KV: v_mfma_f32_16x16x4_f32 with float4 loads split across four k-steps.
-// Softmax statistics are per lane (one query head per lane column); a row max needs two cross-lane steps.
+// Softmax statistics live per lane (one query head per lane column); a row max needs two cross-lane steps.
 
 #include "kv_internal.h"
 
@@ -28,21 +32,18 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 4;
 constexpr float kNegativeInfinity = -__builtin_inff();
 
-__device__ inline float wave_max_across_groups(float value) {
-    value = fmaxf(value, __shfl_xor(value, 16));
-    value = fmaxf(value, __shfl_xor(value, 32));
-    return value;
-}
-
-__device__ inline float wave_sum_across_groups(float value) {
-    value += __shfl_xor(value, 16);
-    value += __shfl_xor(value, 32);
-    return value;
-}
-
 __device__ inline float fast_exp2(float value) { return __builtin_amdgcn_exp2f(value); }
 
-// Element offset of (layer, K|V, kv_head)'s region inside a page.
+__device__ inline float max_across_groups(float value) {
+    value = fmaxf(value, __shfl_xor(value, 16));
+    return fmaxf(value, __shfl_xor(value, 32));
+}
+
+__device__ inline float sum_across_groups(float value) {
+    value += __shfl_xor(value, 16);
+    return value + __shfl_xor(value, 32);
+}
+
 __device__ inline size_t region_offset(const Geometry& g, int which, int kv_head) {
     return ((static_cast<size_t>(g.layer) * 2 + which) * g.kv_heads + kv_head) * static_cast<size_t>(g.page_tokens) *
            g.head_dim;
@@ -55,79 +56,57 @@ struct WaveState {
     float sum;            // this lane's share of the running sum of head r
 };
 
-// Merges the waves of one workgroup and writes the item's result: normalized output for an unsplit token,
-// otherwise the unnormalized output and (max, sum) of every head of the group into the partial row.
 template <int D>
-__device__ void finish_item(const AttentionArgs& a, const DecodeItem& item, WaveState<D>& state, int token_index) {
-    __shared__ float stage_out[kWaves][16][D + 4];
-    __shared__ float stage_max[kWaves][16];
-    __shared__ float stage_sum[kWaves][16];
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int r = lane & 15;
-    const int g = lane >> 4;
-    const float total = wave_sum_across_groups(state.sum);
+__device__ inline void reset(WaveState<D>& state) {
 #pragma unroll
     for (int mt = 0; mt < D / 16; ++mt) {
-        *reinterpret_cast<floatx4*>(&stage_out[wave][r][16 * mt + 4 * g]) = state.out[mt];
+        state.out[mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    if (g == 0) {
-        stage_max[wave][r] = state.maximum;
-        stage_sum[wave][r] = total;
-    }
-    __syncthreads();
-    const Geometry& geo = a.geo;
-    const int group = geo.group;
-    for (int index = threadIdx.x; index < group * D; index += kWaves * 64) {
-        const int head = index / D;
-        const int dim = index - head * D;
-        float maximum = kNegativeInfinity;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            if (stage_sum[w][head] > 0.0f) {
-                maximum = fmaxf(maximum, stage_max[w][head]);
-            }
-        }
-        float value = 0.0f;
-        float sum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            if (stage_sum[w][head] > 0.0f) {
-                const float factor = fast_exp2(stage_max[w][head] - maximum);
-                value += stage_out[w][head][dim] * factor;
-                sum += stage_sum[w][head] * factor;
-            }
-        }
-        if (item.row < 0) {
-            a.output[static_cast<size_t>(token_index) * a.out_stride +
-                     static_cast<size_t>(item.kv_head * group + head) * D + dim] = value / sum;
-        } else {
-            const size_t row = static_cast<size_t>(item.row) * group + head;
-            a.partial_out[row * D + dim] = value;
-            if (dim == 0) {
-                a.partial_ml[row * 2] = maximum;
-                a.partial_ml[row * 2 + 1] = sum;
-            }
-        }
-    }
+    state.maximum = kNegativeInfinity;
+    state.sum = 0.0f;
 }
 
+// Online-softmax update of one 64-key step from its scaled, masked scores (4 tiles of 4 per lane). Returns the
+// factor that rescales the earlier output and replaces the scores with probabilities.
+__device__ inline float softmax_step(floatx4 (&scores)[4], float& maximum, float& sum) {
+    float tile_max = kNegativeInfinity;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            tile_max = fmaxf(tile_max, scores[t][i]);
+        }
+    }
+    tile_max = max_across_groups(tile_max);
+    const float next = fmaxf(maximum, tile_max);
+    const float alpha = fast_exp2(maximum - next);
+    float tile_sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            scores[t][i] = fast_exp2(scores[t][i] - next);
+            tile_sum += scores[t][i];
+        }
+    }
+    sum = sum * alpha + tile_sum;
+    maximum = next;
+    return alpha;
+}
+
+// One token's keys [key_begin, key_end) for one KV head, FP16 pages.
 template <int D>
-__global__ __launch_bounds__(kWaves * 64) void decode_f16_kernel(AttentionArgs a) {
-    const DecodeItem item = a.items[blockIdx.x];
+__device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
     const Geometry& geo = a.geo;
-    const SynapseKvBatchToken token = a.tokens[item.token];
-    const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int r = lane & 15;
     const int g = lane >> 4;
-
     // B operand of S^T = K Q^T: lane (g, r) holds dims 32*ks + 8*g .. +7 of query head r of the group.
     half8 query[D / 32];
     {
         const bool valid = r < geo.group;
-        const float* q = a.qkv + static_cast<size_t>(item.token) * a.qkv_stride +
-                         static_cast<size_t>(item.kv_head * geo.group + (valid ? r : 0)) * D;
+        const float* q = a.qkv + static_cast<size_t>(seg.token) * a.qkv_stride +
+                         static_cast<size_t>(seg.kv_head * geo.group + (valid ? r : 0)) * D;
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
             const floatx4 lo = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g);
@@ -139,24 +118,16 @@ __global__ __launch_bounds__(kWaves * 64) void decode_f16_kernel(AttentionArgs a
             }
         }
     }
-
-    WaveState<D> state;
-#pragma unroll
-    for (int mt = 0; mt < D / 16; ++mt) {
-        state.out[mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    state.maximum = kNegativeInfinity;
-    state.sum = 0.0f;
-
-    const int32_t* table = geo.block_table + static_cast<size_t>(token.slot) * geo.pages_per_slot;
-    const size_t key_region = region_offset(geo, 0, item.kv_head);
-    const size_t value_region = region_offset(geo, 1, item.kv_head);
+    const int slot = a.tokens[seg.token].slot;
+    const int32_t* table = geo.block_table + static_cast<size_t>(slot) * geo.pages_per_slot;
+    const size_t key_region = region_offset(geo, 0, seg.kv_head);
+    const size_t value_region = region_offset(geo, 1, seg.kv_head);
     const int page_tokens = geo.page_tokens;
-    // Row of the A operand this lane loads for QK^T tile (h, u): the permutation that lands key 32h + 8g + 4u + i
-    // of the C tile on this lane group's element 4u + i of the PV B operand.
+    // Row of the A operand this lane loads for QK^T tile (h, u): key 32h + 8*(r/4) + 4u + r%4, so that the C tile
+    // puts key 32h + 8g + 4u + i on this lane group's element 4u + i of the PV B operand.
     const int row_key = 8 * (r >> 2) + (r & 3);
 
-    for (int key0 = item.key_begin + kStepKeys * wave; key0 < item.key_end; key0 += kStepKeys * kWaves) {
+    for (int key0 = seg.key_begin; key0 < seg.key_end; key0 += kStepKeys) {
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
         const _Float16* page = reinterpret_cast<const _Float16*>(
@@ -164,19 +135,14 @@ __global__ __launch_bounds__(kWaves * 64) void decode_f16_kernel(AttentionArgs a
         const _Float16* keys = page + key_region + static_cast<size_t>(within) * D;
         const _Float16* values = page + value_region + within;
 
-        floatx4 scores[4];
+        half8 key_fragment[4][D / 32];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int key = 32 * (t >> 1) + row_key + 4 * (t & 1);
-            half8 fragment[D / 32];
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                fragment[ks] = *reinterpret_cast<const half8*>(keys + static_cast<size_t>(key) * D + 32 * ks + 8 * g);
-            }
-            scores[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) {
-                scores[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fragment[ks], query[ks], scores[t], 0, 0, 0);
+                key_fragment[t][ks] =
+                    *reinterpret_cast<const half8*>(keys + static_cast<size_t>(key) * D + 32 * ks + 8 * g);
             }
         }
         half8 value_fragment[2][D / 16];
@@ -188,34 +154,32 @@ __global__ __launch_bounds__(kWaves * 64) void decode_f16_kernel(AttentionArgs a
                     values + static_cast<size_t>(16 * mt + r) * page_tokens + 32 * h + 8 * g);
             }
         }
-
-        float tile_max = kNegativeInfinity;
+        floatx4 scores[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            scores[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+                scores[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_fragment[t][ks], query[ks], scores[t], 0, 0, 0);
+            }
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int key = key0 + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
-                const float s = key < item.key_end ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
-                scores[t][i] = s;
-                tile_max = fmaxf(tile_max, s);
+                scores[t][i] = key < seg.key_end ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
             }
         }
-        tile_max = wave_max_across_groups(tile_max);
-        const float next = fmaxf(state.maximum, tile_max);
-        const float alpha = fast_exp2(state.maximum - next);
-        float tile_sum = 0.0f;
+        const float alpha = softmax_step(scores, state.maximum, state.sum);
         half8 probability[2];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = fast_exp2(scores[t][i] - next);
-                tile_sum += p;
-                probability[t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(p);
+                probability[t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(scores[t][i]);
             }
         }
-        state.sum = state.sum * alpha + tile_sum;
-        state.maximum = next;
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt) {
             state.out[mt] *= alpha;
@@ -229,46 +193,34 @@ __global__ __launch_bounds__(kWaves * 64) void decode_f16_kernel(AttentionArgs a
             }
         }
     }
-    finish_item<D>(a, item, state, item.token);
 }
 
+// One token's keys [key_begin, key_end) for one KV head, FP32 pages.
 template <int D>
-__global__ __launch_bounds__(kWaves * 64) void decode_f32_kernel(AttentionArgs a) {
-    const DecodeItem item = a.items[blockIdx.x];
+__device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
     const Geometry& geo = a.geo;
-    const SynapseKvBatchToken token = a.tokens[item.token];
-    const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int r = lane & 15;
     const int g = lane >> 4;
-
     // B operand of S^T = K Q^T for k-step (c, i): dim 16*c + 4*g + i of query head r.
     floatx4 query[D / 16];
     {
         const bool valid = r < geo.group;
-        const float* q = a.qkv + static_cast<size_t>(item.token) * a.qkv_stride +
-                         static_cast<size_t>(item.kv_head * geo.group + (valid ? r : 0)) * D;
+        const float* q = a.qkv + static_cast<size_t>(seg.token) * a.qkv_stride +
+                         static_cast<size_t>(seg.kv_head * geo.group + (valid ? r : 0)) * D;
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) {
             const floatx4 v = *reinterpret_cast<const floatx4*>(q + 16 * c + 4 * g);
             query[c] = valid ? v : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
-
-    WaveState<D> state;
-#pragma unroll
-    for (int mt = 0; mt < D / 16; ++mt) {
-        state.out[mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    state.maximum = kNegativeInfinity;
-    state.sum = 0.0f;
-
-    const int32_t* table = geo.block_table + static_cast<size_t>(token.slot) * geo.pages_per_slot;
-    const size_t key_region = region_offset(geo, 0, item.kv_head);
-    const size_t value_region = region_offset(geo, 1, item.kv_head);
+    const int slot = a.tokens[seg.token].slot;
+    const int32_t* table = geo.block_table + static_cast<size_t>(slot) * geo.pages_per_slot;
+    const size_t key_region = region_offset(geo, 0, seg.kv_head);
+    const size_t value_region = region_offset(geo, 1, seg.kv_head);
     const int page_tokens = geo.page_tokens;
 
-    for (int key0 = item.key_begin + kStepKeys * wave; key0 < item.key_end; key0 += kStepKeys * kWaves) {
+    for (int key0 = seg.key_begin; key0 < seg.key_end; key0 += kStepKeys) {
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
         const float* page =
@@ -282,39 +234,23 @@ __global__ __launch_bounds__(kWaves * 64) void decode_f32_kernel(AttentionArgs a
             scores[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int c = 0; c < D / 16; ++c) {
-                const floatx4 k = *reinterpret_cast<const floatx4*>(keys + static_cast<size_t>(16 * t + r) * D + 16 * c + 4 * g);
+                const floatx4 k =
+                    *reinterpret_cast<const floatx4*>(keys + static_cast<size_t>(16 * t + r) * D + 16 * c + 4 * g);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     scores[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(k[i], query[c][i], scores[t], 0, 0, 0);
                 }
             }
         }
-
-        float tile_max = kNegativeInfinity;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int key = key0 + 16 * t + 4 * g + i;
-                const float s = key < item.key_end ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
-                scores[t][i] = s;
-                tile_max = fmaxf(tile_max, s);
+                scores[t][i] = key < seg.key_end ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
             }
         }
-        tile_max = wave_max_across_groups(tile_max);
-        const float next = fmaxf(state.maximum, tile_max);
-        const float alpha = fast_exp2(state.maximum - next);
-        float tile_sum = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                scores[t][i] = fast_exp2(scores[t][i] - next);
-                tile_sum += scores[t][i];
-            }
-        }
-        state.sum = state.sum * alpha + tile_sum;
-        state.maximum = next;
+        const float alpha = softmax_step(scores, state.maximum, state.sum);
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt) {
             state.out[mt] *= alpha;
@@ -333,75 +269,189 @@ __global__ __launch_bounds__(kWaves * 64) void decode_f32_kernel(AttentionArgs a
             }
         }
     }
-    finish_item<D>(a, item, state, item.token);
 }
 
-// Cross-split merge (attention_reduce.metal:5-40) with maxima in log2 units. Grid (merges, heads), head_dim
-// threads.
+// Writes a wave's finished segment: the normalized output of an uncut row, or the segment's partial row (its
+// unnormalized output and, per head, the running max and sum) for the merge kernel.
 template <int D>
-__global__ __launch_bounds__(D) void merge_kernel(AttentionArgs a) {
-    const MergeItem merge = a.merges[blockIdx.x];
-    const int head = blockIdx.y;
+__device__ void finish_segment(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15;
+    const int g = lane >> 4;
     const int group = a.geo.group;
-    const int kv_head = head / group;
-    const int within = head - kv_head * group;
-    const int dim = threadIdx.x;
-    const int first = merge.first_row + kv_head * merge.splits;
-    float maximum = kNegativeInfinity;
-    for (int split = 0; split < merge.splits; ++split) {
-        const size_t row = static_cast<size_t>(first + split) * group + within;
-        if (a.partial_ml[row * 2 + 1] > 0.0f) {
-            maximum = fmaxf(maximum, a.partial_ml[row * 2]);
+    const float total = sum_across_groups(state.sum);
+    if (r >= group) {
+        return;
+    }
+    if (seg.row < 0) {
+        float* destination = a.output + static_cast<size_t>(seg.token) * a.out_stride +
+                             static_cast<size_t>(seg.kv_head * group + r) * D;
+        const float inverse = 1.0f / total;
+#pragma unroll
+        for (int mt = 0; mt < D / 16; ++mt) {
+            *reinterpret_cast<floatx4*>(destination + 16 * mt + 4 * g) = state.out[mt] * inverse;
         }
+        return;
+    }
+    const size_t row = static_cast<size_t>(seg.row) * group + r;
+    float* destination = a.partial_out + row * D;
+#pragma unroll
+    for (int mt = 0; mt < D / 16; ++mt) {
+        *reinterpret_cast<floatx4*>(destination + 16 * mt + 4 * g) = state.out[mt];
+    }
+    if (g == 0) {
+        a.partial_ml[row * 2] = state.maximum;
+        a.partial_ml[row * 2 + 1] = total;
+    }
+}
+
+template <int D, bool F16>
+__global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
+    const int worker = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (worker >= a.workers) {
+        return;
+    }
+    const int first = a.worker_segments[worker];
+    const int last = a.worker_segments[worker + 1];
+    for (int index = first; index < last; ++index) {
+        const DecodeSegment seg = a.segments[index];
+        WaveState<D> state;
+        reset(state);
+        if constexpr (F16) {
+            attend_f16<D>(a, seg, state);
+        } else {
+            attend_f32<D>(a, seg, state);
+        }
+        finish_segment<D>(a, seg, state);
+    }
+}
+
+// Split merge (attention_reduce.metal:5-40): one wave per (merge entry, query head of the group, 64 dims). The
+// lanes first load the (max, sum) of 64 splits at once, reduce the max over splits with a positive sum and turn
+// each split into its weight exp2(m - max); the output is then the weighted sum of the splits' rows over the
+// weighted sums, every row load independent of the others.
+template <int D>
+__global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int first, int count) {
+    const int group = a.geo.group;
+    const int chunks = D / 64;
+    const int job = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (job >= count * group * chunks) {
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    const MergeItem merge = a.merges[first + job / (group * chunks)];
+    const int head = (job / chunks) % group;
+    const int chunk = job % chunks;
+    const float* ml = a.partial_ml;
+    float maximum = kNegativeInfinity;
+    for (int base = 0; base < merge.count; base += 64) {
+        const int split = base + lane;
+        if (split < merge.count) {
+            const size_t row = static_cast<size_t>(merge.first_row + split) * group + head;
+            if (ml[row * 2 + 1] > 0.0f) {
+                maximum = fmaxf(maximum, ml[row * 2]);
+            }
+        }
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        maximum = fmaxf(maximum, __shfl_xor(maximum, offset));
     }
     float sum = 0.0f;
     float value = 0.0f;
-    for (int split = 0; split < merge.splits; ++split) {
-        const size_t row = static_cast<size_t>(first + split) * group + within;
-        const float weight = a.partial_ml[row * 2 + 1];
-        if (weight > 0.0f) {
-            const float factor = fast_exp2(a.partial_ml[row * 2] - maximum);
-            sum += weight * factor;
-            value += a.partial_out[row * D + dim] * factor;
+    for (int base = 0; base < merge.count; base += 64) {
+        const int split = base + lane;
+        float weight = 0.0f;
+        if (split < merge.count) {
+            const size_t row = static_cast<size_t>(merge.first_row + split) * group + head;
+            const float total = ml[row * 2 + 1];
+            weight = total > 0.0f ? fast_exp2(ml[row * 2] - maximum) : 0.0f;
+            sum += total * weight;
+        }
+        const int here = min(64, merge.count - base);
+        const float* rows = a.partial_out + (static_cast<size_t>(merge.first_row + base) * group + head) * D + 64 * chunk + lane;
+        const size_t stride = static_cast<size_t>(group) * D;
+        int split_index = 0;
+        for (; split_index + 4 <= here; split_index += 4) {
+            const float v0 = rows[(split_index + 0) * stride];
+            const float v1 = rows[(split_index + 1) * stride];
+            const float v2 = rows[(split_index + 2) * stride];
+            const float v3 = rows[(split_index + 3) * stride];
+            value += v0 * __shfl(weight, split_index + 0) + v1 * __shfl(weight, split_index + 1) +
+                     v2 * __shfl(weight, split_index + 2) + v3 * __shfl(weight, split_index + 3);
+        }
+        for (; split_index < here; ++split_index) {
+            value += rows[split_index * stride] * __shfl(weight, split_index);
         }
     }
-    a.output[static_cast<size_t>(merge.token) * a.out_stride + static_cast<size_t>(head) * D + dim] = value / sum;
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        sum += __shfl_xor(sum, offset);
+    }
+    a.output[static_cast<size_t>(merge.token) * a.out_stride +
+             static_cast<size_t>(merge.kv_head * group + head) * D + 64 * chunk + lane] = value / sum;
+}
+
+template <int D, bool F16>
+int resident_blocks() {
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_kernel<D, F16>, kWaves * 64, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        return 1;
+    }
+    return blocks > 0 ? blocks : 1;
 }
 
 }  // namespace
 
-hipError_t launch_decode(hipStream_t stream, const AttentionArgs& args, int items, bool fp16) {
-    if (items == 0) {
+int decode_resident_waves(int device, bool fp16, int head_dim) {
+    hipDeviceProp_t properties{};
+    if (hipGetDeviceProperties(&properties, device) != hipSuccess) {
+        (void)hipGetLastError();
+        return 1024;
+    }
+    int blocks = 1;
+    if (fp16) {
+        blocks = head_dim == 128 ? resident_blocks<128, true>() : resident_blocks<64, true>();
+    } else {
+        blocks = head_dim == 128 ? resident_blocks<128, false>() : resident_blocks<64, false>();
+    }
+    return properties.multiProcessorCount * blocks * kWaves;
+}
+
+hipError_t launch_decode(hipStream_t stream, const AttentionArgs& args, bool fp16) {
+    if (args.workers == 0) {
         return hipSuccess;
     }
-    const dim3 grid(items);
+    const dim3 grid((args.workers + kWaves - 1) / kWaves);
     const dim3 block(kWaves * 64);
     const int d = args.geo.head_dim;
     if (fp16) {
         if (d == 128) {
-            hipLaunchKernelGGL(decode_f16_kernel<128>, grid, block, 0, stream, args);
+            hipLaunchKernelGGL((decode_kernel<128, true>), grid, block, 0, stream, args);
         } else {
-            hipLaunchKernelGGL(decode_f16_kernel<64>, grid, block, 0, stream, args);
+            hipLaunchKernelGGL((decode_kernel<64, true>), grid, block, 0, stream, args);
         }
     } else {
         if (d == 128) {
-            hipLaunchKernelGGL(decode_f32_kernel<128>, grid, block, 0, stream, args);
+            hipLaunchKernelGGL((decode_kernel<128, false>), grid, block, 0, stream, args);
         } else {
-            hipLaunchKernelGGL(decode_f32_kernel<64>, grid, block, 0, stream, args);
+            hipLaunchKernelGGL((decode_kernel<64, false>), grid, block, 0, stream, args);
         }
     }
     return hipGetLastError();
 }
 
-hipError_t launch_merge(hipStream_t stream, const AttentionArgs& args, int merges) {
-    if (merges == 0) {
+hipError_t launch_merge(hipStream_t stream, const AttentionArgs& args, int first, int count) {
+    if (count == 0) {
         return hipSuccess;
     }
-    const dim3 grid(merges, args.geo.heads);
+    const int jobs = count * args.geo.group * (args.geo.head_dim / 64);
+    const dim3 grid((jobs + kWaves - 1) / kWaves);
     if (args.geo.head_dim == 128) {
-        hipLaunchKernelGGL(merge_kernel<128>, grid, dim3(128), 0, stream, args);
+        hipLaunchKernelGGL(merge_kernel<128>, grid, dim3(kWaves * 64), 0, stream, args, first, count);
     } else {
-        hipLaunchKernelGGL(merge_kernel<64>, grid, dim3(64), 0, stream, args);
+        hipLaunchKernelGGL(merge_kernel<64>, grid, dim3(kWaves * 64), 0, stream, args, first, count);
     }
     return hipGetLastError();
 }

@@ -175,7 +175,7 @@ struct SynapseKvCache {
     synapse_kv::Dims dims{};
     int device = 0;
     hipStream_t stream = nullptr;
-    uint32_t split_keys = 512;
+    uint32_t split_keys = 256;  // fewest keys per decode wave worker
     uint32_t prefill_runs = 1;
     uint32_t prefill_split_keys = 16384;
 
@@ -210,11 +210,14 @@ struct SynapseKvCache {
     // The current step.
     bool step_ready = false;
     int32_t step_count = 0;
-    int32_t decode_items = 0;
-    int32_t merge_items = 0;
+    int32_t decode_workers = 0;
+    int32_t decode_merges = 0;
+    int32_t prefill_merges = 0;
     int32_t prefill_items = 0;
+    int32_t decode_waves = 1024;  // resident decode waves on the device
     size_t tokens_offset = 0;
-    size_t items_offset = 0;
+    size_t workers_offset = 0;
+    size_t segments_offset = 0;
     size_t merges_offset = 0;
     size_t prefill_offset = 0;
 
@@ -343,35 +346,37 @@ void check_device_pointer(const void* pointer, const char* name) {
 }
 
 // Builds and uploads the attention plan of a prepared step.
+//
+// Lone tokens (and prompt runs of FP32 caches) go to the decode kernel: every (token, KV head) row is cut into
+// 64-key steps, the steps of all rows are laid end to end and split evenly over the resident decode waves, so each
+// wave streams the same number of K/V bytes whatever the ragged lengths. Rows cut by a worker boundary get partial
+// rows and a merge entry. FP16 prompt runs (plan_attention, schedule.rs:34-86: consecutive tokens of one slot at
+// consecutive positions) go to the MFMA prefill kernel in blocks of kPrefillTokens tokens per KV head, their keys
+// split every prefill_split_keys keys and merged by the merge kernel.
 void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t count) {
     const Dims& dims = cache.dims;
-    std::vector<DecodeItem> items;
-    std::vector<MergeItem> merges;
+    struct Row {
+        int32_t token;
+        int32_t kv_head;
+        int32_t keys;
+        int64_t first_step;
+        int64_t steps;
+    };
+    std::vector<Row> rows;
     std::vector<PrefillItem> prefill;
-    int32_t rows = 0;
-    const uint32_t split = cache.split_keys;
+    std::vector<MergeItem> prefill_merges;
+    int32_t partial_rows = 0;
+    int64_t total_steps = 0;
     auto add_decode = [&](int32_t index) {
         const int32_t keys = tokens[index].position + 1;
-        const int32_t splits = (keys + static_cast<int32_t>(split) - 1) / static_cast<int32_t>(split);
-        if (splits <= 1) {
-            for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
-                items.push_back(DecodeItem{index, static_cast<int32_t>(kv_head), 0, keys, -1, {0, 0, 0}});
-            }
-            return;
-        }
-        merges.push_back(MergeItem{index, rows, splits, 0});
+        const int64_t steps = (keys + kStepKeys - 1) / kStepKeys;
         for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
-            for (int32_t part = 0; part < splits; ++part) {
-                const int32_t begin = part * static_cast<int32_t>(split);
-                const int32_t end = std::min(keys, begin + static_cast<int32_t>(split));
-                items.push_back(DecodeItem{index, static_cast<int32_t>(kv_head), begin, end,
-                                           rows + static_cast<int32_t>(kv_head) * splits + part, {0, 0, 0}});
-            }
+            rows.push_back(Row{index, static_cast<int32_t>(kv_head), keys, total_steps, steps});
+            total_steps += steps;
         }
-        rows += splits * static_cast<int32_t>(dims.kv_heads);
     };
-    // Prompt runs (plan_attention, schedule.rs:34-86): consecutive tokens of one slot at consecutive positions.
     int32_t start = 0;
+    std::vector<std::pair<int32_t, int32_t>> runs;
     while (start < count) {
         int32_t end = start + 1;
         while (end < count && tokens[end].slot == tokens[start].slot &&
@@ -383,52 +388,112 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
                 add_decode(index);
             }
         } else {
-            for (int32_t first = start; first < end; first += kPrefillTokens) {
-                const int32_t size = std::min<int32_t>(kPrefillTokens, end - first);
-                const int32_t keys = tokens[first + size - 1].position + 1;
-                const int32_t chunk = static_cast<int32_t>(cache.prefill_split_keys);
-                const int32_t splits = (keys + chunk - 1) / chunk;
-                const int32_t stride = static_cast<int32_t>(dims.kv_heads) * splits;
-                if (splits > 1) {
-                    for (int32_t j = 0; j < size; ++j) {
-                        merges.push_back(MergeItem{first + j, rows + j * stride, splits, 0});
-                    }
-                }
-                for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
-                    for (int32_t part = 0; part < splits; ++part) {
-                        const int32_t begin = part * chunk;
-                        const int32_t finish = std::min(keys, begin + chunk);
-                        const int32_t row = splits > 1 ? rows + static_cast<int32_t>(kv_head) * splits + part : -1;
-                        prefill.push_back(PrefillItem{first, size, static_cast<int32_t>(kv_head), begin, finish, row,
-                                                      stride, 0});
-                    }
-                }
-                if (splits > 1) {
-                    rows += size * stride;
-                }
-            }
+            runs.emplace_back(start, end);
         }
         start = end;
     }
+
+    // Decode: even split of the flattened steps over the wave workers.
+    std::vector<DecodeSegment> segments;
+    std::vector<int32_t> worker_segments;
+    std::vector<MergeItem> merges;
+    int32_t workers = 0;
+    if (total_steps > 0) {
+        const int64_t per_worker_min = std::max<int64_t>(1, cache.split_keys / kStepKeys);
+        const int64_t wanted = std::max<int64_t>(1, total_steps / per_worker_min);
+        workers = static_cast<int32_t>(std::min<int64_t>(std::min<int64_t>(wanted, cache.decode_waves), total_steps));
+        auto boundary = [&](int64_t worker) { return worker * total_steps / workers; };
+        int64_t worker = 0;
+        worker_segments.push_back(0);
+        for (const Row& row : rows) {
+            const size_t first_segment = segments.size();
+            const int64_t row_end = row.first_step + row.steps;
+            int64_t step = row.first_step;
+            while (step < row_end) {
+                while (boundary(worker + 1) <= step) {
+                    ++worker;
+                    worker_segments.push_back(static_cast<int32_t>(segments.size()));
+                }
+                const int64_t stop = std::min<int64_t>(row_end, boundary(worker + 1));
+                const int32_t key_begin = static_cast<int32_t>((step - row.first_step) * kStepKeys);
+                const int32_t key_end =
+                    std::min<int32_t>(row.keys, static_cast<int32_t>((stop - row.first_step) * kStepKeys));
+                segments.push_back(DecodeSegment{row.token, row.kv_head, key_begin, key_end, -1, -1, {0, 0}});
+                step = stop;
+            }
+            const int32_t pieces = static_cast<int32_t>(segments.size() - first_segment);
+            if (pieces > 1) {
+                const int32_t merge = static_cast<int32_t>(merges.size());
+                merges.push_back(MergeItem{row.token, row.kv_head, partial_rows, pieces});
+                for (int32_t piece = 0; piece < pieces; ++piece) {
+                    segments[first_segment + piece].row = partial_rows + piece;
+                    segments[first_segment + piece].merge = merge;
+                }
+                partial_rows += pieces;
+            }
+        }
+        while (static_cast<int32_t>(worker_segments.size()) < workers + 1) {
+            worker_segments.push_back(static_cast<int32_t>(segments.size()));
+        }
+    }
+
+    // Prefill blocks.
+    for (const auto& [run_start, run_end] : runs) {
+        for (int32_t first = run_start; first < run_end; first += kPrefillTokens) {
+            const int32_t size = std::min<int32_t>(kPrefillTokens, run_end - first);
+            const int32_t keys = tokens[first + size - 1].position + 1;
+            const int32_t chunk = static_cast<int32_t>(cache.prefill_split_keys);
+            const int32_t splits = (keys + chunk - 1) / chunk;
+            const int32_t stride = static_cast<int32_t>(dims.kv_heads) * splits;
+            if (splits > 1) {
+                for (int32_t j = 0; j < size; ++j) {
+                    for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
+                        prefill_merges.push_back(MergeItem{first + j, static_cast<int32_t>(kv_head),
+                                                           partial_rows + j * stride +
+                                                               static_cast<int32_t>(kv_head) * splits,
+                                                           splits});
+                    }
+                }
+            }
+            for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
+                for (int32_t part = 0; part < splits; ++part) {
+                    const int32_t begin = part * chunk;
+                    const int32_t finish = std::min(keys, begin + chunk);
+                    const int32_t row = splits > 1 ? partial_rows + static_cast<int32_t>(kv_head) * splits + part : -1;
+                    prefill.push_back(PrefillItem{first, size, static_cast<int32_t>(kv_head), begin, finish, row,
+                                                  stride, 0});
+                }
+            }
+            if (splits > 1) {
+                partial_rows += size * stride;
+            }
+        }
+    }
+    const int32_t decode_merges = static_cast<int32_t>(merges.size());
+    merges.insert(merges.end(), prefill_merges.begin(), prefill_merges.end());
+
     const size_t tokens_bytes = static_cast<size_t>(count) * sizeof(SynapseKvBatchToken);
     cache.tokens_offset = 0;
-    cache.items_offset = align_up(tokens_bytes, 256);
-    cache.merges_offset = align_up(cache.items_offset + items.size() * sizeof(DecodeItem), 256);
+    cache.workers_offset = align_up(tokens_bytes, 256);
+    cache.segments_offset = align_up(cache.workers_offset + worker_segments.size() * sizeof(int32_t), 256);
+    cache.merges_offset = align_up(cache.segments_offset + segments.size() * sizeof(DecodeSegment), 256);
     cache.prefill_offset = align_up(cache.merges_offset + merges.size() * sizeof(MergeItem), 256);
     const size_t total = cache.prefill_offset + prefill.size() * sizeof(PrefillItem);
     cache.blob.ensure(total, "step buffer");
     const size_t group = dims.heads / dims.kv_heads;
-    cache.partial_out.ensure(static_cast<size_t>(rows) * group * dims.head_dim, "attention partials");
-    cache.partial_ml.ensure(static_cast<size_t>(rows) * group * 2, "attention partial statistics");
+    cache.partial_out.ensure(static_cast<size_t>(partial_rows) * group * dims.head_dim, "attention partials");
+    cache.partial_ml.ensure(static_cast<size_t>(partial_rows) * group * 2, "attention partial statistics");
     auto* staging = static_cast<uint8_t*>(cache.uploader.acquire(total));
     std::memcpy(staging + cache.tokens_offset, tokens, tokens_bytes);
-    std::memcpy(staging + cache.items_offset, items.data(), items.size() * sizeof(DecodeItem));
+    std::memcpy(staging + cache.workers_offset, worker_segments.data(), worker_segments.size() * sizeof(int32_t));
+    std::memcpy(staging + cache.segments_offset, segments.data(), segments.size() * sizeof(DecodeSegment));
     std::memcpy(staging + cache.merges_offset, merges.data(), merges.size() * sizeof(MergeItem));
     std::memcpy(staging + cache.prefill_offset, prefill.data(), prefill.size() * sizeof(PrefillItem));
     cache.uploader.copy(cache.blob.pointer, total, cache.stream);
     cache.step_count = count;
-    cache.decode_items = static_cast<int32_t>(items.size());
-    cache.merge_items = static_cast<int32_t>(merges.size());
+    cache.decode_workers = workers;
+    cache.decode_merges = decode_merges;
+    cache.prefill_merges = static_cast<int32_t>(prefill_merges.size());
     cache.prefill_items = static_cast<int32_t>(prefill.size());
     cache.step_ready = true;
 }
@@ -521,6 +586,7 @@ void create_cache(const SynapseKvDesc& desc, SynapseKvCache** output) {
         check_hip(hipMemcpy(cache->device_state.pointer, state, sizeof(state), hipMemcpyHostToDevice), "state upload");
         check_hip(hipMemcpy(cache->cosines.pointer, desc.rope_cosines, rope * 4, hipMemcpyHostToDevice), "RoPE upload");
         check_hip(hipMemcpy(cache->sines.pointer, desc.rope_sines, rope * 4, hipMemcpyHostToDevice), "RoPE upload");
+        cache->decode_waves = decode_resident_waves(cache->device, dims.precision == SYNAPSE_KV_F16, dims.head_dim);
     } catch (...) {
         delete cache;
         throw;
@@ -684,7 +750,7 @@ int32_t synapse_kv_set_option(SynapseKvCache* cache, uint32_t option, uint32_t v
     return guarded([&] {
         if (option == SYNAPSE_KV_OPTION_SPLIT_KEYS) {
             if (value == 0 || value % kStepKeys != 0) {
-                invalid("split keys must be a positive multiple of 64");
+                invalid("decode split keys must be a positive multiple of 64");
             }
             cache->split_keys = value;
         } else if (option == SYNAPSE_KV_OPTION_PREFILL_RUNS) {
@@ -861,15 +927,17 @@ int32_t synapse_kv_attention(SynapseKvCache* cache, uint32_t layer, const float*
         args.output = output;
         args.out_stride = static_cast<int32_t>(out_stride);
         args.scale_log2 = 1.4426950408889634f / std::sqrt(static_cast<float>(dims.head_dim));
-        args.items = reinterpret_cast<const DecodeItem*>(cache->blob.pointer + cache->items_offset);
+        args.workers = cache->decode_workers;
+        args.worker_segments = reinterpret_cast<const int32_t*>(cache->blob.pointer + cache->workers_offset);
+        args.segments = reinterpret_cast<const DecodeSegment*>(cache->blob.pointer + cache->segments_offset);
         args.merges = reinterpret_cast<const MergeItem*>(cache->blob.pointer + cache->merges_offset);
         args.prefill = reinterpret_cast<const PrefillItem*>(cache->blob.pointer + cache->prefill_offset);
         args.partial_out = cache->partial_out.pointer;
         args.partial_ml = cache->partial_ml.pointer;
         const bool fp16 = dims.precision == SYNAPSE_KV_F16;
         check_hip(launch_prefill(cache->stream, args, cache->prefill_items, fp16), "prefill attention");
-        check_hip(launch_decode(cache->stream, args, cache->decode_items, fp16), "decode attention");
-        check_hip(launch_merge(cache->stream, args, cache->merge_items), "split merge");
+        check_hip(launch_decode(cache->stream, args, fp16), "decode attention");
+        check_hip(launch_merge(cache->stream, args, 0, cache->decode_merges + cache->prefill_merges), "split merge");
     });
 }
 

@@ -52,24 +52,25 @@ struct PageArgs {
     int32_t count;
 };
 
-// One decode split-K work item: keys [key_begin, key_end) of one token's slot for one KV head. `row` >= 0 is the
-// partial row of a split token; -1 writes the normalized output directly.
-struct DecodeItem {
+// A decode segment: keys [key_begin, key_end) of one (token, KV head) row. `row` >= 0 is the segment's partial
+// row and `merge` the row's merge entry; row -1 writes the normalized output directly.
+struct DecodeSegment {
     int32_t token;
     int32_t kv_head;
     int32_t key_begin;
     int32_t key_end;
     int32_t row;
-    int32_t pad[3];
+    int32_t merge;
+    int32_t pad[2];
 };
-static_assert(sizeof(DecodeItem) == 32, "DecodeItem is 32 bytes");
+static_assert(sizeof(DecodeSegment) == 32, "DecodeSegment is 32 bytes");
 
-// A split token for the merge: its first partial row and its split count (rows = first + kv_head * splits + s).
+// The partial rows first_row .. first_row + count - 1 of one (token, KV head), merged into the output.
 struct MergeItem {
     int32_t token;
+    int32_t kv_head;
     int32_t first_row;
-    int32_t splits;
-    int32_t pad;
+    int32_t count;
 };
 
 // A prefill work item: `count` (<= kPrefillTokens) consecutive tokens of one prompt run (consecutive positions of
@@ -120,7 +121,9 @@ struct AttentionArgs {
     float* output;
     int32_t out_stride;
     float scale_log2;  // log2(e) / sqrt(head_dim)
-    const DecodeItem* items;
+    int32_t workers;                 // decode wave workers
+    const int32_t* worker_segments;  // [workers + 1]: worker w walks segments [ws[w], ws[w + 1])
+    const DecodeSegment* segments;
     const MergeItem* merges;
     const PrefillItem* prefill;
     float* partial_out;  // [rows][group][head_dim]
@@ -141,8 +144,10 @@ hipError_t launch_table(hipStream_t stream, const TableArgs& args);
 hipError_t launch_zero_pages(hipStream_t stream, const PageArgs& args);
 hipError_t launch_copy_pages(hipStream_t stream, const PageArgs& args);
 hipError_t launch_append(hipStream_t stream, const AppendArgs& args, int tokens, bool fp16);
-hipError_t launch_decode(hipStream_t stream, const AttentionArgs& args, int items, bool fp16);
-hipError_t launch_merge(hipStream_t stream, const AttentionArgs& args, int merges);
+hipError_t launch_decode(hipStream_t stream, const AttentionArgs& args, bool fp16);
+hipError_t launch_merge(hipStream_t stream, const AttentionArgs& args, int first, int count);
+// Waves of the decode kernel that are resident at once on `device` (the persistent worker count).
+int decode_resident_waves(int device, bool fp16, int head_dim);
 hipError_t launch_prefill(hipStream_t stream, const AttentionArgs& args, int items, bool fp16);
 hipError_t launch_gather(hipStream_t stream, const GatherArgs& args, bool fp16);
 
