@@ -123,6 +123,8 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--split-keys", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--separate", action="store_true",
+                        help="append_rope + attention as two launches instead of the fused append_attention")
     parser.add_argument("--cpu-threads", type=int, default=None)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -166,10 +168,14 @@ def main() -> None:
     def step(index: int, events=None) -> None:
         cache.step([(slot, int(lengths[slot]) + index) for slot in range(SEQUENCES)])
         for layer in range(LAYERS):
-            cache.append_rope(layer, qkv[layer])
+            if args.separate:
+                cache.append_rope(layer, qkv[layer])
             if events is not None:
                 events[layer][0].record(stream)
-            cache.attention(layer, qkv[layer], out[layer])
+            if args.separate:
+                cache.attention(layer, qkv[layer], out[layer])
+            else:
+                cache.append_attention(layer, qkv[layer], out[layer])
             if events is not None:
                 events[layer][1].record(stream)
 
@@ -193,6 +199,8 @@ def main() -> None:
     qo_bytes = 2 * SEQUENCES * HEADS * HEAD_DIM * 4
     append_bytes = SEQUENCES * (KV_BYTES_PER_TOKEN_LAYER + 2 * (HEADS + 2 * KV_HEADS) * HEAD_DIM * 4)
     attention_bytes = [keys * KV_BYTES_PER_TOKEN_LAYER + qo_bytes for keys in keys_per_step]
+    if not args.separate:  # the fused launch also writes the new K/V and reads the K/V rows of qkv
+        attention_bytes = [b + SEQUENCES * 2 * KV_BYTES_PER_TOKEN_LAYER for b in attention_bytes]
     step_bytes = [LAYERS * (b + append_bytes) for b in attention_bytes]
     step_gbps = sum(step_bytes) / elapsed / 1e9
     durations = [start.elapsed_time(end) * 1e-3 for step_events in timed_events for start, end in step_events]
@@ -224,7 +232,8 @@ def main() -> None:
         "hbm_frac_of_peak": round(step_gbps / PEAK_HBM_GBPS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode attention (decode_f16_kernel<128> + split merge) per layer",
+            "kernel": ("decode attention (decode_kernel<128, true> + merge_kernel<128>) per layer" if args.separate else
+                       "fused append + decode attention (decode_kernel<128, true> + merge_kernel<128>) per layer"),
             "achieved": round(attention_gbps, 1),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",

@@ -159,6 +159,14 @@ int32_t synapse_kv_append_rope(SynapseKvCache* cache, uint32_t layer, float* qkv
 int32_t synapse_kv_attention(SynapseKvCache* cache, uint32_t layer, const float* qkv, uint32_t qkv_stride,
                              float* output, uint32_t out_stride);
 
+/* synapse_kv_append_rope followed by synapse_kv_attention for one layer, as one decode launch when every token of
+ * the step has its own slot (the decode wave that reads a token's own position rotates and stores its K/V first,
+ * and every wave applies RoPE to Q in registers); otherwise the two launches run in order. `qkv` (device) is read
+ * only: unlike synapse_kv_append_rope, the rotated Q and K are not written back (step/layers.rs:95-96 reads the
+ * rotated rows only for this attention). */
+int32_t synapse_kv_append_attention(SynapseKvCache* cache, uint32_t layer, const float* qkv, uint32_t qkv_stride,
+                                    float* output, uint32_t out_stride);
+
 /* Waits for the cache's stream. */
 int32_t synapse_kv_synchronize(SynapseKvCache* cache);
 

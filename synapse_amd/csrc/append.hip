@@ -5,10 +5,10 @@
 // Qwen2CpuState.cs:85-106): x' = x*c - y*s, y' = x*s + y*c with every product and sum rounded separately (no
 // fused multiply-add), so the result is bit-exact with the CPU path.
 //
-// One workgroup per token. K rows are stored with consecutive lanes on consecutive dims; V is stored transposed
-// ([dim][position] per page region), one 2- or 4-byte store per dim.
+// One workgroup per token; every element goes to its MFMA-fragment slot of the page region (page_layout.h).
 
 #include "kv_internal.h"
+#include "page_layout.h"
 
 // hipcc contracts a*b - c*d into a fused multiply-add by default; the rotation must round every product.
 #pragma clang fp contract(off)
@@ -46,10 +46,12 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     const size_t region = static_cast<size_t>(g.page_tokens) * d;
     const size_t layer_base = static_cast<size_t>(g.layer) * 2 * g.kv_heads;
 
-    const int rotations = (g.heads + g.kv_heads) * half;
+    // Without write-back only the K heads need rotating (Q is rotated where it is consumed).
+    const int first_head = a.write_back ? 0 : g.heads;
+    const int rotations = (g.heads + g.kv_heads - first_head) * half;
     for (int item = threadIdx.x; item < rotations; item += blockDim.x) {
-        const int head = item / half;
-        const int i = item - head * half;
+        const int head = first_head + item / half;
+        const int i = item % half;
         float* values = row + static_cast<size_t>(head) * d;  // K heads follow the Q heads in the row
         const float x = values[i];
         const float y = values[i + half];
@@ -57,13 +59,15 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         const float s = sines[i];
         const float first = x * c - y * s;   // contraction is off for this file: two products, one difference
         const float second = x * s + y * c;
-        values[i] = first;
-        values[i + half] = second;
+        if (a.write_back) {
+            values[i] = first;
+            values[i + half] = second;
+        }
         if (head >= g.heads) {
             const int kv_head = head - g.heads;
-            T* keys = base + (layer_base + kv_head) * region + static_cast<size_t>(within) * d;
-            keys[i] = to_storage<T>(first);
-            keys[i + half] = to_storage<T>(second);
+            T* keys = base + (layer_base + kv_head) * region;
+            keys[key_offset<T>(d, within, i)] = to_storage<T>(first);
+            keys[key_offset<T>(d, within, i + half)] = to_storage<T>(second);
         }
     }
 
@@ -73,7 +77,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         const int kv_head = item / d;
         const int dim = item - kv_head * d;
         T* values = base + (layer_base + g.kv_heads + kv_head) * region;
-        values[static_cast<size_t>(dim) * g.page_tokens + within] = to_storage<T>(value_row[item]);
+        values[value_offset<T>(d, within, dim)] = to_storage<T>(value_row[item]);
     }
 }
 
@@ -94,8 +98,8 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
         const int within = position - logical * g.page_tokens;
         const int page = g.block_table[static_cast<size_t>(a.slot) * g.pages_per_slot + logical];
         const T* base = reinterpret_cast<const T*>(g.pool + static_cast<uint64_t>(page) * g.page_bytes);
-        const T key = base[(layer_base + kv_head) * region + static_cast<size_t>(within) * d + dim];
-        const T value = base[(layer_base + g.kv_heads + kv_head) * region + static_cast<size_t>(dim) * g.page_tokens + within];
+        const T key = base[(layer_base + kv_head) * region + key_offset<T>(d, within, dim)];
+        const T value = base[(layer_base + g.kv_heads + kv_head) * region + value_offset<T>(d, within, dim)];
         reinterpret_cast<T*>(a.keys)[index] = key;
         reinterpret_cast<T*>(a.values)[index] = value;
     }

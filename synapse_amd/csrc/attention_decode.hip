@@ -22,6 +22,7 @@
 // Softmax statistics live per lane (one query head per lane column); a row max needs two cross-lane steps.
 
 #include "kv_internal.h"
+#include "page_layout.h"
 
 namespace synapse_kv {
 namespace {
@@ -33,6 +34,19 @@ constexpr int kWaves = 4;
 constexpr float kNegativeInfinity = -__builtin_inff();
 
 __device__ inline float fast_exp2(float value) { return __builtin_amdgcn_exp2f(value); }
+
+// Qwen2RopeTable.Apply (Qwen2CpuState.cs:85-106) for one pair: separately rounded products and sums, so the
+// rotated values are bit-exact with the CPU path.
+__device__ inline void rotate_pair(float x, float y, float c, float s, float& first, float& second) {
+#pragma clang fp contract(off)
+    first = x * c - y * s;
+    second = x * s + y * c;
+}
+
+template <typename T>
+__device__ inline T load_fragment(const T* pointer) {
+    return __builtin_nontemporal_load(pointer);  // K/V stream through once per launch
+}
 
 __device__ inline float max_across_groups(float value) {
     value = fmaxf(value, __shfl_xor(value, 16));
@@ -101,20 +115,43 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
     const int lane = threadIdx.x & 63;
     const int r = lane & 15;
     const int g = lane >> 4;
-    // B operand of S^T = K Q^T: lane (g, r) holds dims 32*ks + 8*g .. +7 of query head r of the group.
+    // B operand of S^T = K Q^T: lane (g, r) holds dims 32*ks + 8*g .. +7 of query head r of the group. With
+    // D/2 = 32 * (D/64) the RoPE partner of dim i < D/2 (i + D/2) sits in the same lane at ks + D/64.
     half8 query[D / 32];
     {
         const bool valid = r < geo.group;
         const float* q = a.qkv + static_cast<size_t>(seg.token) * a.qkv_stride +
                          static_cast<size_t>(seg.kv_head * geo.group + (valid ? r : 0)) * D;
+        float values[D / 32][8];
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
             const floatx4 lo = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g);
             const floatx4 hi = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g + 4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                query[ks][j] = valid ? static_cast<_Float16>(lo[j]) : static_cast<_Float16>(0.0f);
-                query[ks][j + 4] = valid ? static_cast<_Float16>(hi[j]) : static_cast<_Float16>(0.0f);
+                values[ks][j] = lo[j];
+                values[ks][j + 4] = hi[j];
+            }
+        }
+        if (a.rotate) {
+            const int position = a.tokens[seg.token].position;
+            const float* cosines = a.cosines + static_cast<size_t>(position) * (D / 2);
+            const float* sines = a.sines + static_cast<size_t>(position) * (D / 2);
+#pragma unroll
+            for (int ks = 0; ks < D / 64; ++ks) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int i = 32 * ks + 8 * g + j;
+                    rotate_pair(values[ks][j], values[ks + D / 64][j], cosines[i], sines[i], values[ks][j],
+                                values[ks + D / 64][j]);
+                }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                query[ks][j] = valid ? static_cast<_Float16>(values[ks][j]) : static_cast<_Float16>(0.0f);
             }
         }
     }
@@ -123,26 +160,25 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
     const size_t key_region = region_offset(geo, 0, seg.kv_head);
     const size_t value_region = region_offset(geo, 1, seg.kv_head);
     const int page_tokens = geo.page_tokens;
-    // Row of the A operand this lane loads for QK^T tile (h, u): key 32h + 8*(r/4) + 4u + r%4, so that the C tile
-    // puts key 32h + 8g + 4u + i on this lane group's element 4u + i of the PV B operand.
-    const int row_key = 8 * (r >> 2) + (r & 3);
+    // The A operand of QK^T tile t = 2h + u holds key 32h + 8*(r/4) + 4u + r%4 in row r (the page layout stores it
+    // there), so the C tile puts key 32h + 8g + 4u + i on this lane group's element 4u + i of the PV B operand.
 
     for (int key0 = seg.key_begin; key0 < seg.key_end; key0 += kStepKeys) {
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
         const _Float16* page = reinterpret_cast<const _Float16*>(
             geo.pool + static_cast<uint64_t>(table[logical]) * geo.page_bytes);
-        const _Float16* keys = page + key_region + static_cast<size_t>(within) * D;
-        const _Float16* values = page + value_region + within;
+        // 64-key blocks in fragment order: every load below is one contiguous 1 KiB wave load.
+        const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D) + lane;
+        const half8* values =
+            reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D) + lane;
 
         half8 key_fragment[4][D / 32];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const int key = 32 * (t >> 1) + row_key + 4 * (t & 1);
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                key_fragment[t][ks] =
-                    *reinterpret_cast<const half8*>(keys + static_cast<size_t>(key) * D + 32 * ks + 8 * g);
+                key_fragment[t][ks] = load_fragment(keys + (t * (D / 32) + ks) * 64);
             }
         }
         half8 value_fragment[2][D / 16];
@@ -150,8 +186,7 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int mt = 0; mt < D / 16; ++mt) {
-                value_fragment[h][mt] = *reinterpret_cast<const half8*>(
-                    values + static_cast<size_t>(16 * mt + r) * page_tokens + 32 * h + 8 * g);
+                value_fragment[h][mt] = load_fragment(values + (h * (D / 16) + mt) * 64);
             }
         }
         floatx4 scores[4];
@@ -202,7 +237,8 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
     const int lane = threadIdx.x & 63;
     const int r = lane & 15;
     const int g = lane >> 4;
-    // B operand of S^T = K Q^T for k-step (c, i): dim 16*c + 4*g + i of query head r.
+    // B operand of S^T = K Q^T for k-step (c, i): dim 16*c + 4*g + i of query head r. The RoPE partner of dim
+    // i < D/2 sits in the same lane at c + D/32.
     floatx4 query[D / 16];
     {
         const bool valid = r < geo.group;
@@ -210,8 +246,30 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
                          static_cast<size_t>(seg.kv_head * geo.group + (valid ? r : 0)) * D;
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) {
-            const floatx4 v = *reinterpret_cast<const floatx4*>(q + 16 * c + 4 * g);
-            query[c] = valid ? v : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            query[c] = *reinterpret_cast<const floatx4*>(q + 16 * c + 4 * g);
+        }
+        if (a.rotate) {
+            const int position = a.tokens[seg.token].position;
+            const float* cosines = a.cosines + static_cast<size_t>(position) * (D / 2);
+            const float* sines = a.sines + static_cast<size_t>(position) * (D / 2);
+#pragma unroll
+            for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int index = 16 * c + 4 * g + i;
+                    float first;
+                    float second;
+                    rotate_pair(query[c][i], query[c + D / 32][i], cosines[index], sines[index], first, second);
+                    query[c][i] = first;
+                    query[c + D / 32][i] = second;
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+            if (!valid) {
+                query[c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
         }
     }
     const int slot = a.tokens[seg.token].slot;
@@ -225,8 +283,10 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
         const int within = key0 - logical * page_tokens;
         const float* page =
             reinterpret_cast<const float*>(geo.pool + static_cast<uint64_t>(table[logical]) * geo.page_bytes);
-        const float* keys = page + key_region + static_cast<size_t>(within) * D;
-        const float* values = page + value_region + within;
+        const floatx4* keys =
+            reinterpret_cast<const floatx4*>(page + key_region + static_cast<size_t>(within) * D) + lane;
+        const floatx4* values =
+            reinterpret_cast<const floatx4*>(page + value_region + static_cast<size_t>(within) * D) + lane;
 
         floatx4 scores[4];
 #pragma unroll
@@ -234,8 +294,7 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
             scores[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int c = 0; c < D / 16; ++c) {
-                const floatx4 k =
-                    *reinterpret_cast<const floatx4*>(keys + static_cast<size_t>(16 * t + r) * D + 16 * c + 4 * g);
+                const floatx4 k = load_fragment(keys + (t * (D / 16) + c) * 64);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     scores[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(k[i], query[c][i], scores[t], 0, 0, 0);
@@ -260,8 +319,7 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
             for (int mt = 0; mt < D / 16; ++mt) {
-                const floatx4 v = *reinterpret_cast<const floatx4*>(
-                    values + static_cast<size_t>(16 * mt + r) * page_tokens + 16 * t + 4 * g);
+                const floatx4 v = load_fragment(values + (t * (D / 16) + mt) * 64);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     state.out[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[i], scores[t][i], state.out[mt], 0, 0, 0);
@@ -305,6 +363,38 @@ __device__ void finish_segment(const AttentionArgs& a, const DecodeSegment& seg,
     }
 }
 
+// Fused append (synapse_rope_kv, elementwise.metal:73-126) of one (token, KV head) by the wave that owns the row's
+// last segment, i.e. the only wave that reads the token's own position: rotate K, store K and V in the page's
+// element type, then make the stores visible to this wave's loads. The qkv rows are read, not rewritten.
+template <typename T, int D>
+__device__ void append_row(const AttentionArgs& a, const DecodeSegment& seg) {
+    const Geometry& geo = a.geo;
+    const int lane = threadIdx.x & 63;
+    const SynapseKvBatchToken token = a.tokens[seg.token];
+    const int logical = token.position / geo.page_tokens;
+    const int within = token.position - logical * geo.page_tokens;
+    const int32_t page = geo.block_table[static_cast<size_t>(token.slot) * geo.pages_per_slot + logical];
+    T* base = reinterpret_cast<T*>(const_cast<uint8_t*>(geo.pool) + static_cast<uint64_t>(page) * geo.page_bytes);
+    T* keys = base + region_offset(geo, 0, seg.kv_head);
+    T* values = base + region_offset(geo, 1, seg.kv_head);
+    const float* row = a.qkv + static_cast<size_t>(seg.token) * a.qkv_stride;
+    const float* key = row + static_cast<size_t>(geo.heads + seg.kv_head) * D;
+    const float* value = row + static_cast<size_t>(geo.heads + geo.kv_heads + seg.kv_head) * D;
+    const float* cosines = a.cosines + static_cast<size_t>(token.position) * (D / 2);
+    const float* sines = a.sines + static_cast<size_t>(token.position) * (D / 2);
+    for (int i = lane; i < D / 2; i += 64) {
+        float first;
+        float second;
+        rotate_pair(key[i], key[i + D / 2], cosines[i], sines[i], first, second);
+        keys[key_offset<T>(D, within, i)] = static_cast<T>(first);
+        keys[key_offset<T>(D, within, i + D / 2)] = static_cast<T>(second);
+    }
+    for (int dim = lane; dim < D; dim += 64) {
+        values[value_offset<T>(D, within, dim)] = static_cast<T>(value[dim]);
+    }
+    __threadfence();
+}
+
 template <int D, bool F16>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
     const int worker = blockIdx.x * kWaves + (threadIdx.x >> 6);
@@ -315,6 +405,13 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
     const int last = a.worker_segments[worker + 1];
     for (int index = first; index < last; ++index) {
         const DecodeSegment seg = a.segments[index];
+        if (a.append && seg.key_end == a.tokens[seg.token].position + 1) {
+            if constexpr (F16) {
+                append_row<_Float16, D>(a, seg);
+            } else {
+                append_row<float, D>(a, seg);
+            }
+        }
         WaveState<D> state;
         reset(state);
         if constexpr (F16) {

@@ -24,6 +24,13 @@ constexpr float kNegativeInfinity = -__builtin_inff();
 
 __device__ inline float fast_exp2(float value) { return __builtin_amdgcn_exp2f(value); }
 
+// Qwen2RopeTable.Apply (Qwen2CpuState.cs:85-106) for one pair, products and sums rounded separately.
+__device__ inline void rotate_pair(float x, float y, float c, float s, float& first, float& second) {
+#pragma clang fp contract(off)
+    first = x * c - y * s;
+    second = x * s + y * c;
+}
+
 template <int D>
 __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
     constexpr int NT = kPrefillTiles;
@@ -37,22 +44,45 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
     const SynapseKvBatchToken first = a.tokens[item.first_token];
     const int first_position = first.position;
 
-    // B operands of S^T = K Q^T: tile c, lane (g, r) holds dims 32*ks + 8*g .. +7 of token 16*c + r.
+    // B operands of S^T = K Q^T: tile c, lane (g, r) holds dims 32*ks + 8*g .. +7 of token 16*c + r; the RoPE
+    // partner of dim i < D/2 is in the same lane at ks + D/64.
     half8 query[NT][D / 32];
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
         const int j = 16 * c + r;
         const bool valid = j < item.count;
-        const float* q = a.qkv + static_cast<size_t>(item.first_token + (valid ? j : 0)) * a.qkv_stride +
-                         static_cast<size_t>(head) * D;
+        const int token = item.first_token + (valid ? j : 0);
+        const float* q = a.qkv + static_cast<size_t>(token) * a.qkv_stride + static_cast<size_t>(head) * D;
+        float values[D / 32][8];
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
             const floatx4 lo = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g);
             const floatx4 hi = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g + 4);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                query[c][ks][e] = valid ? static_cast<_Float16>(lo[e]) : static_cast<_Float16>(0.0f);
-                query[c][ks][e + 4] = valid ? static_cast<_Float16>(hi[e]) : static_cast<_Float16>(0.0f);
+                values[ks][e] = lo[e];
+                values[ks][e + 4] = hi[e];
+            }
+        }
+        if (a.rotate) {
+            const int position = first_position + (valid ? j : 0);
+            const float* cosines = a.cosines + static_cast<size_t>(position) * (D / 2);
+            const float* sines = a.sines + static_cast<size_t>(position) * (D / 2);
+#pragma unroll
+            for (int ks = 0; ks < D / 64; ++ks) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int i = 32 * ks + 8 * g + e;
+                    rotate_pair(values[ks][e], values[ks + D / 64][e], cosines[i], sines[i], values[ks][e],
+                                values[ks + D / 64][e]);
+                }
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                query[c][ks][e] = valid ? static_cast<_Float16>(values[ks][e]) : static_cast<_Float16>(0.0f);
             }
         }
     }
@@ -75,7 +105,6 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
     const size_t key_region = ((static_cast<size_t>(geo.layer) * 2) * geo.kv_heads + item.kv_head) * region;
     const size_t value_region = ((static_cast<size_t>(geo.layer) * 2 + 1) * geo.kv_heads + item.kv_head) * region;
     const int page_tokens = geo.page_tokens;
-    const int row_key = 8 * (r >> 2) + (r & 3);
     // Keys past the block's last token are masked for every column.
     const int key_stop = min(item.key_end, first_position + item.count);
 
@@ -84,17 +113,19 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
         const int within = key0 - logical * page_tokens;
         const _Float16* page = reinterpret_cast<const _Float16*>(
             geo.pool + static_cast<uint64_t>(table[logical]) * geo.page_bytes);
-        const _Float16* keys = page + key_region + static_cast<size_t>(within) * D;
-        const _Float16* values = page + value_region + within;
+        // Fragment-ordered 64-key blocks (page_layout.h); plain cached loads, since every query block of the run
+        // reads the same keys.
+        const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D) + lane;
+        const half8* values =
+            reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D) + lane;
 
         floatx4 scores[NT][4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const int key = 32 * (t >> 1) + row_key + 4 * (t & 1);
             half8 fragment[D / 32];
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                fragment[ks] = *reinterpret_cast<const half8*>(keys + static_cast<size_t>(key) * D + 32 * ks + 8 * g);
+                fragment[ks] = keys[(t * (D / 32) + ks) * 64];
             }
 #pragma unroll
             for (int c = 0; c < NT; ++c) {
@@ -148,8 +179,7 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
             half8 value_fragment[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                value_fragment[h] = *reinterpret_cast<const half8*>(
-                    values + static_cast<size_t>(16 * mt + r) * page_tokens + 32 * h + 8 * g);
+                value_fragment[h] = values[(h * (D / 16) + mt) * 64];
             }
 #pragma unroll
             for (int c = 0; c < NT; ++c) {

@@ -215,6 +215,7 @@ struct SynapseKvCache {
     int32_t prefill_merges = 0;
     int32_t prefill_items = 0;
     int32_t decode_waves = 1024;  // resident decode waves on the device
+    bool fusable = false;         // the step can append and attend in one decode launch
     size_t tokens_offset = 0;
     size_t workers_offset = 0;
     size_t segments_offset = 0;
@@ -495,6 +496,14 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.decode_merges = decode_merges;
     cache.prefill_merges = static_cast<int32_t>(prefill_merges.size());
     cache.prefill_items = static_cast<int32_t>(prefill.size());
+    // The fused append + decode launch needs every token to own its slot: no token may read another token's
+    // position of the same step, and each (token, KV head) row appends its own position only.
+    std::vector<int32_t> slots(count);
+    for (int32_t index = 0; index < count; ++index) {
+        slots[index] = tokens[index].slot;
+    }
+    std::sort(slots.begin(), slots.end());
+    cache.fusable = prefill.empty() && std::adjacent_find(slots.begin(), slots.end()) == slots.end();
     cache.step_ready = true;
 }
 
@@ -676,6 +685,70 @@ void require_step(const SynapseKvCache& cache, uint32_t layer) {
     if (layer >= cache.dims.layers) {
         invalid("layer " + std::to_string(layer) + " is outside 0.." + std::to_string(cache.dims.layers - 1));
     }
+}
+
+void launch_append_layer(SynapseKvCache& cache, uint32_t layer, float* qkv, uint32_t qkv_stride, bool write_back) {
+    const Dims& dims = cache.dims;
+    AppendArgs args{};
+    args.geo = geometry(cache, layer);
+    args.pool = cache.pool;
+    args.tokens = reinterpret_cast<const SynapseKvBatchToken*>(cache.blob.pointer + cache.tokens_offset);
+    args.qkv = qkv;
+    args.qkv_stride = static_cast<int32_t>(qkv_stride);
+    args.half_dim = static_cast<int32_t>(dims.head_dim / 2);
+    args.cosines = cache.cosines.pointer;
+    args.sines = cache.sines.pointer;
+    args.write_back = write_back ? 1 : 0;
+    check_hip(launch_append(cache.stream, args, cache.step_count, dims.precision == SYNAPSE_KV_F16), "append");
+}
+
+// Attention of the prepared step for one layer; with `append`, the step's K/V are appended first (fused into the
+// decode launch when the step allows it).
+void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint32_t qkv_stride, float* output,
+                   uint32_t out_stride, bool append) {
+    require_step(cache, layer);
+    const Dims& dims = cache.dims;
+    const uint32_t needed = (append ? dims.heads + 2 * dims.kv_heads : dims.heads) * dims.head_dim;
+    if (qkv_stride < needed || qkv_stride % 4 != 0) {
+        invalid("qkv_stride must be a multiple of 4 and hold the row's " + std::to_string(needed) + " values");
+    }
+    if (out_stride < dims.heads * dims.head_dim) {
+        invalid("out_stride is shorter than heads * head_dim");
+    }
+    if (reinterpret_cast<uintptr_t>(qkv) % 16 != 0) {
+        invalid("qkv must be 16-byte aligned");
+    }
+    set_device(cache);
+    check_device_pointer(qkv, "qkv");
+    check_device_pointer(output, "output");
+    // With `append`, qkv stays as the caller wrote it: K is rotated on its way into the pages and Q in registers.
+    const bool fused = append && cache.fusable;
+    if (append && !fused) {
+        launch_append_layer(cache, layer, const_cast<float*>(qkv), qkv_stride, false);
+    }
+    AttentionArgs args{};
+    args.geo = geometry(cache, layer);
+    args.tokens = reinterpret_cast<const SynapseKvBatchToken*>(cache.blob.pointer + cache.tokens_offset);
+    args.qkv = qkv;
+    args.qkv_stride = static_cast<int32_t>(qkv_stride);
+    args.output = output;
+    args.out_stride = static_cast<int32_t>(out_stride);
+    args.scale_log2 = 1.4426950408889634f / std::sqrt(static_cast<float>(dims.head_dim));
+    args.rotate = append ? 1 : 0;
+    args.append = fused ? 1 : 0;
+    args.cosines = cache.cosines.pointer;
+    args.sines = cache.sines.pointer;
+    args.workers = cache.decode_workers;
+    args.worker_segments = reinterpret_cast<const int32_t*>(cache.blob.pointer + cache.workers_offset);
+    args.segments = reinterpret_cast<const DecodeSegment*>(cache.blob.pointer + cache.segments_offset);
+    args.merges = reinterpret_cast<const MergeItem*>(cache.blob.pointer + cache.merges_offset);
+    args.prefill = reinterpret_cast<const PrefillItem*>(cache.blob.pointer + cache.prefill_offset);
+    args.partial_out = cache.partial_out.pointer;
+    args.partial_ml = cache.partial_ml.pointer;
+    const bool fp16 = dims.precision == SYNAPSE_KV_F16;
+    check_hip(launch_prefill(cache.stream, args, cache.prefill_items, fp16), "prefill attention");
+    check_hip(launch_decode(cache.stream, args, fp16), "decode attention");
+    check_hip(launch_merge(cache.stream, args, 0, cache.decode_merges + cache.prefill_merges), "split merge");
 }
 
 }  // namespace
@@ -886,16 +959,7 @@ int32_t synapse_kv_append_rope(SynapseKvCache* cache, uint32_t layer, float* qkv
         }
         set_device(*cache);
         check_device_pointer(qkv, "qkv");
-        AppendArgs args{};
-        args.geo = geometry(*cache, layer);
-        args.pool = cache->pool;
-        args.tokens = reinterpret_cast<const SynapseKvBatchToken*>(cache->blob.pointer + cache->tokens_offset);
-        args.qkv = qkv;
-        args.qkv_stride = static_cast<int32_t>(qkv_stride);
-        args.half_dim = static_cast<int32_t>(dims.head_dim / 2);
-        args.cosines = cache->cosines.pointer;
-        args.sines = cache->sines.pointer;
-        check_hip(launch_append(cache->stream, args, cache->step_count, dims.precision == SYNAPSE_KV_F16), "append");
+        launch_append_layer(*cache, layer, qkv, qkv_stride, true);
     });
 }
 
@@ -904,41 +968,15 @@ int32_t synapse_kv_attention(SynapseKvCache* cache, uint32_t layer, const float*
     if (cache == nullptr || qkv == nullptr || output == nullptr) {
         return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache, qkv or output");
     }
-    return guarded([&] {
-        require_step(*cache, layer);
-        const Dims& dims = cache->dims;
-        if (qkv_stride < dims.heads * dims.head_dim || qkv_stride % 4 != 0) {
-            invalid("qkv_stride must be a multiple of 4 and hold heads * head_dim query values");
-        }
-        if (out_stride < dims.heads * dims.head_dim) {
-            invalid("out_stride is shorter than heads * head_dim");
-        }
-        if (reinterpret_cast<uintptr_t>(qkv) % 16 != 0) {
-            invalid("qkv must be 16-byte aligned");
-        }
-        set_device(*cache);
-        check_device_pointer(qkv, "qkv");
-        check_device_pointer(output, "output");
-        AttentionArgs args{};
-        args.geo = geometry(*cache, layer);
-        args.tokens = reinterpret_cast<const SynapseKvBatchToken*>(cache->blob.pointer + cache->tokens_offset);
-        args.qkv = qkv;
-        args.qkv_stride = static_cast<int32_t>(qkv_stride);
-        args.output = output;
-        args.out_stride = static_cast<int32_t>(out_stride);
-        args.scale_log2 = 1.4426950408889634f / std::sqrt(static_cast<float>(dims.head_dim));
-        args.workers = cache->decode_workers;
-        args.worker_segments = reinterpret_cast<const int32_t*>(cache->blob.pointer + cache->workers_offset);
-        args.segments = reinterpret_cast<const DecodeSegment*>(cache->blob.pointer + cache->segments_offset);
-        args.merges = reinterpret_cast<const MergeItem*>(cache->blob.pointer + cache->merges_offset);
-        args.prefill = reinterpret_cast<const PrefillItem*>(cache->blob.pointer + cache->prefill_offset);
-        args.partial_out = cache->partial_out.pointer;
-        args.partial_ml = cache->partial_ml.pointer;
-        const bool fp16 = dims.precision == SYNAPSE_KV_F16;
-        check_hip(launch_prefill(cache->stream, args, cache->prefill_items, fp16), "prefill attention");
-        check_hip(launch_decode(cache->stream, args, fp16), "decode attention");
-        check_hip(launch_merge(cache->stream, args, 0, cache->decode_merges + cache->prefill_merges), "split merge");
-    });
+    return guarded([&] { run_attention(*cache, layer, qkv, qkv_stride, output, out_stride, false); });
+}
+
+int32_t synapse_kv_append_attention(SynapseKvCache* cache, uint32_t layer, const float* qkv, uint32_t qkv_stride,
+                                    float* output, uint32_t out_stride) {
+    if (cache == nullptr || qkv == nullptr || output == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache, qkv or output");
+    }
+    return guarded([&] { run_attention(*cache, layer, qkv, qkv_stride, output, out_stride, true); });
 }
 
 int32_t synapse_kv_synchronize(SynapseKvCache* cache) {

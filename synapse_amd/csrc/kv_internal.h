@@ -111,6 +111,7 @@ struct AppendArgs {
     int32_t half_dim;
     const float* cosines;
     const float* sines;
+    int32_t write_back;  // 1: rotated Q and K replace the qkv values; 0: qkv is left as it was
 };
 
 struct AttentionArgs {
@@ -121,6 +122,10 @@ struct AttentionArgs {
     float* output;
     int32_t out_stride;
     float scale_log2;  // log2(e) / sqrt(head_dim)
+    int32_t rotate;    // 1: Q in qkv is unrotated; the decode kernel applies RoPE in registers
+    int32_t append;    // 1: the decode kernel also appends each row's own K/V (fused step)
+    const float* cosines;
+    const float* sines;
     int32_t workers;                 // decode wave workers
     const int32_t* worker_segments;  // [workers + 1]: worker w walks segments [ws[w], ws[w + 1])
     const DecodeSegment* segments;
@@ -138,6 +143,8 @@ struct GatherArgs {
     uint8_t* keys;    // [count][kv_heads][head_dim] in the storage type
     uint8_t* values;  // [count][kv_heads][head_dim] in the storage type
 };
+
+// Page regions are stored in MFMA-fragment order; see page_layout.h.
 
 // Launchers (each enqueues on `stream` and returns the launch status).
 hipError_t launch_table(hipStream_t stream, const TableArgs& args);

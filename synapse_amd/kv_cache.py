@@ -232,6 +232,15 @@ class PagedKvCache:
             self.library.c_attention(self.handle, layer, _address(qkv), q_stride, _address(output), o_stride)
         )
 
+    def append_attention(self, layer: int, qkv, output, qkv_stride: int | None = None,
+                         out_stride: int | None = None) -> None:
+        """append_rope + attention in one call (one launch when every token owns its slot); qkv is read only."""
+        q_stride = self.qkv_width if qkv_stride is None else qkv_stride
+        o_stride = self.heads * self.head_dim if out_stride is None else out_stride
+        self.library.check(
+            self.library.c_append_attention(self.handle, layer, _address(qkv), q_stride, _address(output), o_stride)
+        )
+
     def synchronize(self) -> None:
         self.library.check(self.library.c_synchronize(self.handle))
 

@@ -136,6 +136,7 @@ EXPORTS = {
     "synapse_kv_step": (_I32, [_P, ctypes.POINTER(BatchToken), _SIZE]),
     "synapse_kv_append_rope": (_I32, [_P, _U32, _P, _U32]),
     "synapse_kv_attention": (_I32, [_P, _U32, _P, _U32, _P, _U32]),
+    "synapse_kv_append_attention": (_I32, [_P, _U32, _P, _U32, _P, _U32]),
     "synapse_kv_synchronize": (_I32, [_P]),
     "synapse_kv_slot_info": (
         _I32,

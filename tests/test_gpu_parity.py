@@ -56,8 +56,9 @@ class Pair:
         assert status == expected, (name, args, status, expected)
         return status
 
-    def step(self, tokens, rng, attend=True):
-        """One step: prepare, then per layer append (+ attention); checks every output."""
+    def step(self, tokens, rng, attend=True, fused=False):
+        """One step: prepare, then per layer append (+ attention); checks every output. `fused` drives the layer
+        through append_attention (qkv stays unrotated) instead of append_rope + attention."""
         torch = self.torch
         status = self.call("step", tokens)
         if status:
@@ -66,13 +67,21 @@ class Pair:
         for layer in range(self.layers):
             rows = rng.standard_normal((count, self.width)).astype(np.float32)
             qkv = torch.from_numpy(rows.copy()).cuda()
-            self.gpu.append_rope(layer, qkv)
+            original = rows.copy()
+            out = torch.full((count, self.heads * self.head_dim), float("nan"), device="cuda")
+            if fused:
+                self.gpu.append_attention(layer, qkv, out)
+            else:
+                self.gpu.append_rope(layer, qkv)
             assert self.cpu.append_rope(layer, rows, self.cos, self.sin) == 0
-            rotated = qkv.cpu().numpy()
-            assert np.array_equal(rotated.view(np.uint32), rows.view(np.uint32)), "rotated Q/K differ"
-            if attend:
-                out = torch.full((count, self.heads * self.head_dim), float("nan"), device="cuda")
-                self.gpu.attention(layer, qkv, out)
+            if fused:
+                assert np.array_equal(qkv.cpu().numpy().view(np.uint32), original.view(np.uint32)), "qkv changed"
+            else:
+                rotated = qkv.cpu().numpy()
+                assert np.array_equal(rotated.view(np.uint32), rows.view(np.uint32)), "rotated Q/K differ"
+            if attend or fused:
+                if not fused:
+                    self.gpu.attention(layer, qkv, out)
                 expected = np.zeros((count, self.heads * self.head_dim), dtype=np.float32)
                 self.cpu.attention(layer, rows, expected)
                 got = out.cpu().numpy()
@@ -141,6 +150,31 @@ def test_decode_steps_match_the_restatement(torch_gpu, heads, kv_heads, head_dim
         assert pair.step(tokens, rng) == 0
         lengths = [length + 1 for length in lengths]
     pair.check_tables()
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,precision,page", SHAPES[:4])
+def test_append_attention_matches_the_restatement(torch_gpu, heads, kv_heads, head_dim, precision, page):
+    say("append_attention parity", heads, kv_heads, head_dim, precision, page)
+    pair = Pair(torch_gpu, heads=heads, kv_heads=kv_heads, head_dim=head_dim, precision=precision, page=page,
+                growth=max(page, 256), max_pages=96 if page == 64 else 48)
+    rng = np.random.default_rng(head_dim + 7)
+    lengths = [0, 257, 600]
+    for slot, length in enumerate(lengths):
+        for first in range(0, length, 200):
+            assert pair.step([(slot, p) for p in range(first, min(length, first + 200))], rng, attend=False) == 0
+    # Decode steps with one token per slot: one fused launch per layer, split and unsplit rows.
+    for split in (256, 64):
+        pair.gpu.set_split_keys(split)
+        assert pair.step([(slot, lengths[slot]) for slot in range(3)], rng, fused=True) == 0
+        lengths = [length + 1 for length in lengths]
+    # Two tokens of one slot and a prompt run: the append runs first, then attention, qkv still untouched.
+    assert pair.step([(0, lengths[0]), (0, lengths[0] + 5), (1, lengths[1])], rng, fused=True) == 0
+    lengths[0] += 6
+    lengths[1] += 1
+    assert pair.step([(2, p) for p in range(lengths[2], lengths[2] + 40)] + [(1, lengths[1])], rng, fused=True) == 0
+    pair.check_tables()
+    for slot in range(3):
+        pair.check_contents(slot)
 
 
 def test_single_position_and_page_boundaries(torch_gpu):
