@@ -123,6 +123,7 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--split-keys", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--prefetch", type=int, default=None, help="decode kernel variant (0 or 1)")
     parser.add_argument("--separate", action="store_true",
                         help="append_rope + attention as two launches instead of the fused append_attention")
     parser.add_argument("--cpu-threads", type=int, default=None)
@@ -153,6 +154,10 @@ def main() -> None:
     cache.set_stream(stream)
     if args.split_keys:
         cache.set_split_keys(args.split_keys)
+    if args.prefetch is not None:
+        from synapse_amd.native import OPTION_DECODE_PREFETCH
+
+        cache.set_option(OPTION_DECODE_PREFETCH, args.prefetch)
     for slot, length in enumerate(lengths.tolist()):
         cache.reserve(slot, length + total_steps + 1)
     generator = torch.Generator(device="cuda")
@@ -165,47 +170,51 @@ def main() -> None:
     qkv = torch.empty((LAYERS, SEQUENCES, width), device="cuda").normal_(generator=generator)
     out = torch.empty((LAYERS, SEQUENCES, HEADS * HEAD_DIM), device="cuda")
 
-    def step(index: int, events=None) -> None:
+    def step(index: int) -> None:
         cache.step([(slot, int(lengths[slot]) + index) for slot in range(SEQUENCES)])
         for layer in range(LAYERS):
             if args.separate:
                 cache.append_rope(layer, qkv[layer])
-            if events is not None:
-                events[layer][0].record(stream)
-            if args.separate:
                 cache.attention(layer, qkv[layer], out[layer])
             else:
                 cache.append_attention(layer, qkv[layer], out[layer])
-            if events is not None:
-                events[layer][1].record(stream)
 
     for index in range(args.warmup):
         step(index)
     torch.cuda.synchronize()
-    timed_events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                     for _ in range(LAYERS)] for _ in range(args.steps)]
+    # Kernel times come from the library's profile mode: sampled dispatches of the cache record HIP events around
+    # themselves on the cache's stream (hipExtLaunchKernel), read back after the timed region. Every layer launches
+    # identical work, so two launches of each kind per step are timed; timing all 56 would add queue time.
+    from synapse_amd.native import OPTION_PROFILE_EVERY
+
+    cache.set_option(OPTION_PROFILE_EVERY, LAYERS // 2)
+    cache.profile_begin()
     torch.cuda.synchronize()
     begin = time.perf_counter()
     for index in range(args.steps):
-        step(args.warmup + index, timed_events[index])
+        step(args.warmup + index)
+    host_seconds = time.perf_counter() - begin  # time to enqueue the timed steps (host side)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - begin
+    kernels = cache.profile_end()
 
     ms_per_step = elapsed * 1e3 / args.steps
     tokens_per_second = SEQUENCES * args.steps / elapsed
     # Algorithmic bytes: each step reads the K/V of every attended position once per layer and writes the new
     # token's K/V; q/out rows are read/written once (fp32).
     keys_per_step = [int((lengths + args.warmup + index + 1).sum()) for index in range(args.steps)]
-    qo_bytes = 2 * SEQUENCES * HEADS * HEAD_DIM * 4
-    append_bytes = SEQUENCES * (KV_BYTES_PER_TOKEN_LAYER + 2 * (HEADS + 2 * KV_HEADS) * HEAD_DIM * 4)
-    attention_bytes = [keys * KV_BYTES_PER_TOKEN_LAYER + qo_bytes for keys in keys_per_step]
-    if not args.separate:  # the fused launch also writes the new K/V and reads the K/V rows of qkv
-        attention_bytes = [b + SEQUENCES * 2 * KV_BYTES_PER_TOKEN_LAYER for b in attention_bytes]
-    step_bytes = [LAYERS * (b + append_bytes) for b in attention_bytes]
+    q_bytes = SEQUENCES * HEADS * HEAD_DIM * 4
+    kv_row_bytes = SEQUENCES * 2 * KV_HEADS * HEAD_DIM * 4  # the new token's fp32 K and V rows
+    append_bytes = SEQUENCES * KV_BYTES_PER_TOKEN_LAYER  # the new token's FP16 K and V
+    # Decode launch (fused append): every attended position's K/V read once, the new K/V written, Q and the new
+    # K/V rows read. The step adds the output rows (written by the merge or directly).
+    decode_bytes = [keys * KV_BYTES_PER_TOKEN_LAYER + append_bytes + q_bytes + kv_row_bytes for keys in keys_per_step]
+    step_bytes = [LAYERS * (b + q_bytes) for b in decode_bytes]
     step_gbps = sum(step_bytes) / elapsed / 1e9
-    durations = [start.elapsed_time(end) * 1e-3 for step_events in timed_events for start, end in step_events]
-    attention_seconds = statistics.mean(durations)
-    attention_gbps = statistics.mean(attention_bytes) / attention_seconds / 1e9
+    decode_launches, decode_ms = kernels["decode"]
+    decode_seconds = decode_ms * 1e-3 / decode_launches
+    decode_gbps = statistics.mean(decode_bytes) / decode_seconds / 1e9
+    merge_launches, merge_ms = kernels.get("merge", (0, 0.0))
     traffic = measured_traffic()
 
     result = {
@@ -229,18 +238,22 @@ def main() -> None:
             "page_tokens": PAGE_TOKENS, "lengths": lengths.tolist(), "parallelism": "single GPU",
         },
         "hbm_gbps": round(step_gbps, 1),
+        "host_ms_per_step": round(host_seconds * 1e3 / args.steps, 4),
         "hbm_frac_of_peak": round(step_gbps / PEAK_HBM_GBPS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": ("decode attention (decode_kernel<128, true> + merge_kernel<128>) per layer" if args.separate else
-                       "fused append + decode attention (decode_kernel<128, true> + merge_kernel<128>) per layer"),
-            "achieved": round(attention_gbps, 1),
+            "kernel": ("decode_kernel<128, true, true> (split-K decode)" if args.separate else
+                       "decode_kernel<128, true, true> (fused append + split-K decode)"),
+            "achieved": round(decode_gbps, 1),
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
-            "frac": round(attention_gbps / PEAK_HBM_GBPS, 4),
+            "frac": round(decode_gbps / PEAK_HBM_GBPS, 4),
             "traffic": traffic["bytes_per_launch"] if traffic else None,
-            "algorithmic_bytes_per_launch": int(statistics.mean(attention_bytes)),
-            "avg_launch_us": round(attention_seconds * 1e6, 2),
+            "algorithmic_bytes_per_launch": int(statistics.mean(decode_bytes)),
+            "avg_launch_us": round(decode_seconds * 1e6, 2),
+            "timed_launches": decode_launches,
+            "merge_avg_launch_us": round(merge_ms * 1e3 / merge_launches, 2) if merge_launches else None,
+            "kernels_ms": {kind: round(ms, 3) for kind, (count, ms) in kernels.items()},
         },
     }
     if not args.no_cpu_baseline:

@@ -43,6 +43,8 @@ extern "C" {
 #define SYNAPSE_KV_OPTION_SPLIT_KEYS 1u     /* fewest keys per decode wave worker; a multiple of 64 (default 256) */
 #define SYNAPSE_KV_OPTION_PREFILL_RUNS 2u   /* 1: FP16 prompt runs use the MFMA prefill kernel (default); 0: decode path */
 #define SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS 3u /* keys per prefill split-K work item; a multiple of 64 (default 16384) */
+#define SYNAPSE_KV_OPTION_DECODE_PREFETCH 4u /* 1: FP16 decode keeps the next step's loads in flight (two register sets) */
+#define SYNAPSE_KV_OPTION_PROFILE_EVERY 5u   /* profile mode times every n-th launch of each kernel kind (default 1) */
 
 /* GpuDeviceInfo (native/synapse-gpu/src/Features/GpuKernels/mod.rs:20-31), 152 bytes. */
 typedef struct SynapseKvDeviceInfo {
@@ -95,6 +97,19 @@ typedef struct SynapseKvPageStats {
     uint32_t device_status; /* 0, or the first inconsistency the table kernel found */
     uint32_t reserved;
 } SynapseKvPageStats;
+
+/* GPU time per kernel kind between synapse_kv_profile_begin and _end, 128 bytes. */
+#define SYNAPSE_KV_KERNEL_TABLE 0   /* block-table operations */
+#define SYNAPSE_KV_KERNEL_PAGES 1   /* page zero-fill and copy-on-write copies */
+#define SYNAPSE_KV_KERNEL_APPEND 2  /* RoPE + KV append */
+#define SYNAPSE_KV_KERNEL_DECODE 3  /* split-K decode attention (with the fused append when used) */
+#define SYNAPSE_KV_KERNEL_MERGE 4   /* split merge */
+#define SYNAPSE_KV_KERNEL_PREFILL 5 /* prompt-run attention */
+#define SYNAPSE_KV_KERNEL_GATHER 6  /* KV read-back */
+typedef struct SynapseKvProfile {
+    uint64_t launches[8];
+    double milliseconds[8];
+} SynapseKvProfile;
 
 typedef struct SynapseKvCache SynapseKvCache;
 
@@ -167,6 +182,14 @@ int32_t synapse_kv_attention(SynapseKvCache* cache, uint32_t layer, const float*
 int32_t synapse_kv_append_attention(SynapseKvCache* cache, uint32_t layer, const float* qkv, uint32_t qkv_stride,
                                     float* output, uint32_t out_stride);
 
+/* Per-kernel GPU time, as SYNAPSE_GPU_PROFILE does for the Metal backend (metal/encoder.rs:161-182): between
+ * _begin and _end every launch of the cache records HIP events around its own dispatch on the cache's stream;
+ * _end waits for the stream and returns launch counts and summed milliseconds per SYNAPSE_KV_KERNEL_* kind.
+ * With SYNAPSE_KV_OPTION_PROFILE_EVERY = n only every n-th launch of a kind is timed and counted (each timed
+ * dispatch costs a few microseconds of queue time). */
+int32_t synapse_kv_profile_begin(SynapseKvCache* cache);
+int32_t synapse_kv_profile_end(SynapseKvCache* cache, SynapseKvProfile* profile);
+
 /* Waits for the cache's stream. */
 int32_t synapse_kv_synchronize(SynapseKvCache* cache);
 
@@ -199,11 +222,13 @@ static_assert(sizeof(SynapseKvDeviceInfo) == 152, "SynapseKvDeviceInfo is pinned
 static_assert(sizeof(SynapseKvBatchToken) == 16, "SynapseKvBatchToken is pinned at 16 bytes");
 static_assert(sizeof(SynapseKvDesc) == 64, "SynapseKvDesc is pinned at 64 bytes");
 static_assert(sizeof(SynapseKvPageStats) == 40, "SynapseKvPageStats is pinned at 40 bytes");
+static_assert(sizeof(SynapseKvProfile) == 128, "SynapseKvProfile is pinned at 128 bytes");
 #else
 _Static_assert(sizeof(SynapseKvDeviceInfo) == 152, "SynapseKvDeviceInfo is pinned at 152 bytes");
 _Static_assert(sizeof(SynapseKvBatchToken) == 16, "SynapseKvBatchToken is pinned at 16 bytes");
 _Static_assert(sizeof(SynapseKvDesc) == 64, "SynapseKvDesc is pinned at 64 bytes");
 _Static_assert(sizeof(SynapseKvPageStats) == 40, "SynapseKvPageStats is pinned at 40 bytes");
+_Static_assert(sizeof(SynapseKvProfile) == 128, "SynapseKvProfile is pinned at 128 bytes");
 #endif
 
 #endif /* SYNAPSE_KV_H */

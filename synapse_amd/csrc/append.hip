@@ -107,19 +107,19 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 
 }  // namespace
 
-hipError_t launch_append(hipStream_t stream, const AppendArgs& args, int tokens, bool fp16) {
+hipError_t launch_append(const Launch& launch, const AppendArgs& args, int tokens, bool fp16) {
     if (tokens == 0) {
         return hipSuccess;
     }
     if (fp16) {
-        hipLaunchKernelGGL(append_kernel<_Float16>, dim3(tokens), dim3(256), 0, stream, args);
+        SYNAPSE_KV_LAUNCH(append_kernel<_Float16>, dim3(tokens), dim3(256), launch, args);
     } else {
-        hipLaunchKernelGGL(append_kernel<float>, dim3(tokens), dim3(256), 0, stream, args);
+        SYNAPSE_KV_LAUNCH(append_kernel<float>, dim3(tokens), dim3(256), launch, args);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_gather(hipStream_t stream, const GatherArgs& args, bool fp16) {
+hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16) {
     const size_t total = static_cast<size_t>(args.geo.kv_heads) * args.geo.head_dim * args.count;
     if (total == 0) {
         return hipSuccess;
@@ -127,9 +127,9 @@ hipError_t launch_gather(hipStream_t stream, const GatherArgs& args, bool fp16) 
     const size_t blocks = (total + 255) / 256;
     const dim3 grid(static_cast<unsigned>(blocks < 4096 ? blocks : 4096));
     if (fp16) {
-        hipLaunchKernelGGL(gather_kernel<_Float16>, grid, dim3(256), 0, stream, args);
+        SYNAPSE_KV_LAUNCH(gather_kernel<_Float16>, grid, dim3(256), launch, args);
     } else {
-        hipLaunchKernelGGL(gather_kernel<float>, grid, dim3(256), 0, stream, args);
+        SYNAPSE_KV_LAUNCH(gather_kernel<float>, grid, dim3(256), launch, args);
     }
     return hipGetLastError();
 }

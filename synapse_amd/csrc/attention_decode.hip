@@ -108,8 +108,15 @@ __device__ inline float softmax_step(floatx4 (&scores)[4], float& maximum, float
     return alpha;
 }
 
-// One token's keys [key_begin, key_end) for one KV head, FP16 pages.
 template <int D>
+struct Fragments16 {
+    half8 key[4][D / 32];
+    half8 value[2][D / 16];
+};
+
+// One token's keys [key_begin, key_end) for one KV head, FP16 pages. With PREFETCH the next step's fragments are
+// loaded before the current step is computed.
+template <int D, bool PREFETCH>
 __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
     const Geometry& geo = a.geo;
     const int lane = threadIdx.x & 63;
@@ -163,7 +170,7 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
     // The A operand of QK^T tile t = 2h + u holds key 32h + 8*(r/4) + 4u + r%4 in row r (the page layout stores it
     // there), so the C tile puts key 32h + 8g + 4u + i on this lane group's element 4u + i of the PV B operand.
 
-    for (int key0 = seg.key_begin; key0 < seg.key_end; key0 += kStepKeys) {
+    auto fetch = [&](int key0, Fragments16<D>& fragments) {
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
         const _Float16* page = reinterpret_cast<const _Float16*>(
@@ -172,30 +179,30 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
         const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D) + lane;
         const half8* values =
             reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D) + lane;
-
-        half8 key_fragment[4][D / 32];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                key_fragment[t][ks] = load_fragment(keys + (t * (D / 32) + ks) * 64);
+                fragments.key[t][ks] = load_fragment(keys + (t * (D / 32) + ks) * 64);
             }
         }
-        half8 value_fragment[2][D / 16];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int mt = 0; mt < D / 16; ++mt) {
-                value_fragment[h][mt] = load_fragment(values + (h * (D / 16) + mt) * 64);
+                fragments.value[h][mt] = load_fragment(values + (h * (D / 16) + mt) * 64);
             }
         }
+    };
+    auto consume = [&](int key0, const Fragments16<D>& fragments) {
         floatx4 scores[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             scores[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                scores[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(key_fragment[t][ks], query[ks], scores[t], 0, 0, 0);
+                scores[t] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(fragments.key[t][ks], query[ks], scores[t], 0, 0, 0);
             }
         }
 #pragma unroll
@@ -223,9 +230,42 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int mt = 0; mt < D / 16; ++mt) {
-                state.out[mt] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(value_fragment[h][mt], probability[h], state.out[mt], 0, 0, 0);
+                state.out[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fragments.value[h][mt], probability[h],
+                                                                       state.out[mt], 0, 0, 0);
             }
+        }
+    };
+    if constexpr (!PREFETCH) {
+        for (int key0 = seg.key_begin; key0 < seg.key_end; key0 += kStepKeys) {
+            Fragments16<D> fragments;
+            fetch(key0, fragments);
+            consume(key0, fragments);
+        }
+    } else {
+        // Two register sets: the loads of the next step are in flight while the current step computes.
+        Fragments16<D> even;
+        Fragments16<D> odd;
+        int key0 = seg.key_begin;
+        fetch(key0, even);
+        while (true) {
+            const bool more = key0 + kStepKeys < seg.key_end;
+            if (more) {
+                fetch(key0 + kStepKeys, odd);
+            }
+            consume(key0, even);
+            if (!more) {
+                break;
+            }
+            key0 += kStepKeys;
+            const bool after = key0 + kStepKeys < seg.key_end;
+            if (after) {
+                fetch(key0 + kStepKeys, even);
+            }
+            consume(key0, odd);
+            if (!after) {
+                break;
+            }
+            key0 += kStepKeys;
         }
     }
 }
@@ -395,7 +435,7 @@ __device__ void append_row(const AttentionArgs& a, const DecodeSegment& seg) {
     __threadfence();
 }
 
-template <int D, bool F16>
+template <int D, bool F16, bool PREFETCH>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
     const int worker = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (worker >= a.workers) {
@@ -415,7 +455,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
         WaveState<D> state;
         reset(state);
         if constexpr (F16) {
-            attend_f16<D>(a, seg, state);
+            attend_f16<D, PREFETCH>(a, seg, state);
         } else {
             attend_f32<D>(a, seg, state);
         }
@@ -440,45 +480,66 @@ __global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int
     const int head = (job / chunks) % group;
     const int chunk = job % chunks;
     const float* ml = a.partial_ml;
-    float maximum = kNegativeInfinity;
-    for (int base = 0; base < merge.count; base += 64) {
-        const int split = base + lane;
-        if (split < merge.count) {
-            const size_t row = static_cast<size_t>(merge.first_row + split) * group + head;
-            if (ml[row * 2 + 1] > 0.0f) {
-                maximum = fmaxf(maximum, ml[row * 2]);
-            }
-        }
-    }
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        maximum = fmaxf(maximum, __shfl_xor(maximum, offset));
-    }
+    const size_t stride = static_cast<size_t>(group) * D;
     float sum = 0.0f;
     float value = 0.0f;
-    for (int base = 0; base < merge.count; base += 64) {
-        const int split = base + lane;
-        float weight = 0.0f;
-        if (split < merge.count) {
-            const size_t row = static_cast<size_t>(merge.first_row + split) * group + head;
-            const float total = ml[row * 2 + 1];
-            weight = total > 0.0f ? fast_exp2(ml[row * 2] - maximum) : 0.0f;
-            sum += total * weight;
+    if (merge.count <= 64) {
+        // One round of loads: every split's row value and (max, sum) are requested before any is used.
+        const float* rows = a.partial_out + (static_cast<size_t>(merge.first_row) * group + head) * D + 64 * chunk + lane;
+        float values[64];
+#pragma unroll
+        for (int split = 0; split < 64; ++split) {
+            values[split] = split < merge.count ? rows[split * stride] : 0.0f;
         }
-        const int here = min(64, merge.count - base);
-        const float* rows = a.partial_out + (static_cast<size_t>(merge.first_row + base) * group + head) * D + 64 * chunk + lane;
-        const size_t stride = static_cast<size_t>(group) * D;
-        int split_index = 0;
-        for (; split_index + 4 <= here; split_index += 4) {
-            const float v0 = rows[(split_index + 0) * stride];
-            const float v1 = rows[(split_index + 1) * stride];
-            const float v2 = rows[(split_index + 2) * stride];
-            const float v3 = rows[(split_index + 3) * stride];
-            value += v0 * __shfl(weight, split_index + 0) + v1 * __shfl(weight, split_index + 1) +
-                     v2 * __shfl(weight, split_index + 2) + v3 * __shfl(weight, split_index + 3);
+        float split_max = kNegativeInfinity;
+        float split_sum = 0.0f;
+        if (lane < merge.count) {
+            const size_t row = static_cast<size_t>(merge.first_row + lane) * group + head;
+            split_max = ml[row * 2];
+            split_sum = ml[row * 2 + 1];
         }
-        for (; split_index < here; ++split_index) {
-            value += rows[split_index * stride] * __shfl(weight, split_index);
+        float maximum = split_sum > 0.0f ? split_max : kNegativeInfinity;
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            maximum = fmaxf(maximum, __shfl_xor(maximum, offset));
+        }
+        const float weight = split_sum > 0.0f ? fast_exp2(split_max - maximum) : 0.0f;
+        sum = split_sum * weight;
+#pragma unroll
+        for (int split = 0; split < 64; ++split) {
+            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, weight), split));
+            value += values[split] * w;
+        }
+    } else {
+        float maximum = kNegativeInfinity;
+        for (int base = 0; base < merge.count; base += 64) {
+            const int split = base + lane;
+            if (split < merge.count) {
+                const size_t row = static_cast<size_t>(merge.first_row + split) * group + head;
+                if (ml[row * 2 + 1] > 0.0f) {
+                    maximum = fmaxf(maximum, ml[row * 2]);
+                }
+            }
+        }
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            maximum = fmaxf(maximum, __shfl_xor(maximum, offset));
+        }
+        for (int base = 0; base < merge.count; base += 64) {
+            const int split = base + lane;
+            float weight = 0.0f;
+            if (split < merge.count) {
+                const size_t row = static_cast<size_t>(merge.first_row + split) * group + head;
+                const float total = ml[row * 2 + 1];
+                weight = total > 0.0f ? fast_exp2(ml[row * 2] - maximum) : 0.0f;
+                sum += total * weight;
+            }
+            const int here = min(64, merge.count - base);
+            const float* rows =
+                a.partial_out + (static_cast<size_t>(merge.first_row + base) * group + head) * D + 64 * chunk + lane;
+            for (int index = 0; index < here; ++index) {
+                value += rows[index * stride] * __shfl(weight, index);
+            }
         }
     }
 #pragma unroll
@@ -489,10 +550,11 @@ __global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int
              static_cast<size_t>(merge.kv_head * group + head) * D + 64 * chunk + lane] = value / sum;
 }
 
-template <int D, bool F16>
+template <int D, bool F16, bool PREFETCH>
 int resident_blocks() {
     int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_kernel<D, F16>, kWaves * 64, 0) != hipSuccess) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_kernel<D, F16, PREFETCH>, kWaves * 64, 0) !=
+        hipSuccess) {
         (void)hipGetLastError();
         return 1;
     }
@@ -501,54 +563,62 @@ int resident_blocks() {
 
 }  // namespace
 
-int decode_resident_waves(int device, bool fp16, int head_dim) {
+int decode_resident_waves(int device, bool fp16, int head_dim, bool prefetch) {
     hipDeviceProp_t properties{};
     if (hipGetDeviceProperties(&properties, device) != hipSuccess) {
         (void)hipGetLastError();
         return 1024;
     }
     int blocks = 1;
-    if (fp16) {
-        blocks = head_dim == 128 ? resident_blocks<128, true>() : resident_blocks<64, true>();
+    if (fp16 && prefetch) {
+        blocks = head_dim == 128 ? resident_blocks<128, true, true>() : resident_blocks<64, true, true>();
+    } else if (fp16) {
+        blocks = head_dim == 128 ? resident_blocks<128, true, false>() : resident_blocks<64, true, false>();
     } else {
-        blocks = head_dim == 128 ? resident_blocks<128, false>() : resident_blocks<64, false>();
+        blocks = head_dim == 128 ? resident_blocks<128, false, false>() : resident_blocks<64, false, false>();
     }
     return properties.multiProcessorCount * blocks * kWaves;
 }
 
-hipError_t launch_decode(hipStream_t stream, const AttentionArgs& args, bool fp16) {
+hipError_t launch_decode(const Launch& launch, const AttentionArgs& args, bool fp16, bool prefetch) {
     if (args.workers == 0) {
         return hipSuccess;
     }
     const dim3 grid((args.workers + kWaves - 1) / kWaves);
     const dim3 block(kWaves * 64);
     const int d = args.geo.head_dim;
-    if (fp16) {
+    if (fp16 && prefetch) {
         if (d == 128) {
-            hipLaunchKernelGGL((decode_kernel<128, true>), grid, block, 0, stream, args);
+            SYNAPSE_KV_LAUNCH((decode_kernel<128, true, true>), grid, block, launch, args);
         } else {
-            hipLaunchKernelGGL((decode_kernel<64, true>), grid, block, 0, stream, args);
+            SYNAPSE_KV_LAUNCH((decode_kernel<64, true, true>), grid, block, launch, args);
+        }
+    } else if (fp16) {
+        if (d == 128) {
+            SYNAPSE_KV_LAUNCH((decode_kernel<128, true, false>), grid, block, launch, args);
+        } else {
+            SYNAPSE_KV_LAUNCH((decode_kernel<64, true, false>), grid, block, launch, args);
         }
     } else {
         if (d == 128) {
-            hipLaunchKernelGGL((decode_kernel<128, false>), grid, block, 0, stream, args);
+            SYNAPSE_KV_LAUNCH((decode_kernel<128, false, false>), grid, block, launch, args);
         } else {
-            hipLaunchKernelGGL((decode_kernel<64, false>), grid, block, 0, stream, args);
+            SYNAPSE_KV_LAUNCH((decode_kernel<64, false, false>), grid, block, launch, args);
         }
     }
     return hipGetLastError();
 }
 
-hipError_t launch_merge(hipStream_t stream, const AttentionArgs& args, int first, int count) {
+hipError_t launch_merge(const Launch& launch, const AttentionArgs& args, int first, int count) {
     if (count == 0) {
         return hipSuccess;
     }
     const int jobs = count * args.geo.group * (args.geo.head_dim / 64);
     const dim3 grid((jobs + kWaves - 1) / kWaves);
     if (args.geo.head_dim == 128) {
-        hipLaunchKernelGGL(merge_kernel<128>, grid, dim3(kWaves * 64), 0, stream, args, first, count);
+        SYNAPSE_KV_LAUNCH(merge_kernel<128>, grid, dim3(kWaves * 64), launch, args, first, count);
     } else {
-        hipLaunchKernelGGL(merge_kernel<64>, grid, dim3(kWaves * 64), 0, stream, args, first, count);
+        SYNAPSE_KV_LAUNCH(merge_kernel<64>, grid, dim3(kWaves * 64), launch, args, first, count);
     }
     return hipGetLastError();
 }

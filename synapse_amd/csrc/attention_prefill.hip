@@ -228,7 +228,7 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
 
 }  // namespace
 
-hipError_t launch_prefill(hipStream_t stream, const AttentionArgs& args, int items, bool fp16) {
+hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int items, bool fp16) {
     if (items == 0) {
         return hipSuccess;
     }
@@ -238,9 +238,9 @@ hipError_t launch_prefill(hipStream_t stream, const AttentionArgs& args, int ite
     const dim3 grid(items);
     const dim3 block(args.geo.group * 64);
     if (args.geo.head_dim == 128) {
-        hipLaunchKernelGGL(prefill_f16_kernel<128>, grid, block, 0, stream, args);
+        SYNAPSE_KV_LAUNCH(prefill_f16_kernel<128>, grid, block, launch, args);
     } else {
-        hipLaunchKernelGGL(prefill_f16_kernel<64>, grid, block, 0, stream, args);
+        SYNAPSE_KV_LAUNCH(prefill_f16_kernel<64>, grid, block, launch, args);
     }
     return hipGetLastError();
 }

@@ -178,6 +178,7 @@ struct SynapseKvCache {
     uint32_t split_keys = 256;  // fewest keys per decode wave worker
     uint32_t prefill_runs = 1;
     uint32_t prefill_split_keys = 16384;
+    uint32_t prefetch = 1;  // decode kernel variant: 1 = two register sets, next step's loads in flight
 
     // Host shadow of the allocator (same rules as the table kernel).
     std::vector<uint32_t> capacity;
@@ -207,6 +208,16 @@ struct SynapseKvCache {
     int32_t fresh_count = 0;
     int32_t copy_count = 0;
 
+    // Profiling (synapse_kv_profile_begin/end): an event pair per launch, reused from a pool.
+    bool profiling = false;
+    uint32_t profile_every = 1;       // time every n-th launch of each kind
+    uint64_t profile_seen[8] = {};    // launches of each kind since profiling began
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> event_pool;
+    std::vector<std::pair<int, size_t>> profiled;  // (kernel kind, event pair index)
+
+    // Device addresses that passed the device-memory check, most recent first.
+    std::vector<const void*> checked_pointers;
+
     // The current step.
     bool step_ready = false;
     int32_t step_count = 0;
@@ -226,6 +237,10 @@ struct SynapseKvCache {
         (void)hipSetDevice(device);
         (void)hipStreamSynchronize(stream);
         uploader.release();
+        for (auto& pair : event_pool) {
+            (void)hipEventDestroy(pair.first);
+            (void)hipEventDestroy(pair.second);
+        }
         block_table.reset();
         device_refcount.reset();
         device_free.reset();
@@ -246,6 +261,52 @@ struct SynapseKvCache {
 
 namespace synapse_kv {
 namespace {
+
+// The launch target of a kernel of `kind` that will be dispatched (`dispatched` false: no kernel follows, so no
+// events are taken).
+Launch launch_for(SynapseKvCache& cache, int kind, bool dispatched) {
+    Launch launch{cache.stream, nullptr, nullptr};
+    if (!cache.profiling || !dispatched || cache.profile_seen[kind]++ % cache.profile_every != 0) {
+        return launch;
+    }
+    const size_t index = cache.profiled.size();
+    if (index == cache.event_pool.size()) {
+        hipEvent_t start = nullptr;
+        hipEvent_t stop = nullptr;
+        check_hip(hipEventCreate(&start), "profile event");
+        if (hipEventCreate(&stop) != hipSuccess) {
+            (void)hipEventDestroy(start);
+            check_hip(hipErrorOutOfMemory, "profile event");
+        }
+        cache.event_pool.emplace_back(start, stop);
+    }
+    cache.profiled.emplace_back(kind, index);
+    launch.start = cache.event_pool[index].first;
+    launch.stop = cache.event_pool[index].second;
+    return launch;
+}
+
+// Rejects host memory for a device operand. The runtime query is slow next to a kernel launch, so addresses that
+// passed are remembered (a layer's qkv and output buffers are reused every step).
+void check_device_pointer(SynapseKvCache& cache, const void* pointer, const char* name) {
+    if (pointer == nullptr) {
+        fail(SYNAPSE_KV_NULL_POINTER, std::string("null pointer: ") + name);
+    }
+    auto& seen = cache.checked_pointers;
+    const auto found = std::find(seen.begin(), seen.end(), pointer);
+    if (found != seen.end()) {
+        return;
+    }
+    hipPointerAttribute_t attributes{};
+    if (hipPointerGetAttributes(&attributes, pointer) != hipSuccess || attributes.type != hipMemoryTypeDevice) {
+        (void)hipGetLastError();
+        invalid(std::string(name) + " must be device memory");
+    }
+    if (seen.size() >= 256) {
+        seen.pop_back();
+    }
+    seen.insert(seen.begin(), pointer);
+}
 
 uint32_t pages_for(const Dims& dims, uint32_t positions) { return (positions + dims.page_tokens - 1) / dims.page_tokens; }
 
@@ -308,11 +369,11 @@ void flush_ops(SynapseKvCache& cache) {
     args.state = cache.device_state.pointer;
     args.fresh = cache.fresh.pointer;
     args.copies = cache.copies.pointer;
-    check_hip(launch_table(cache.stream, args), "table kernel");
+    check_hip(launch_table(launch_for(cache, SYNAPSE_KV_KERNEL_TABLE, args.op_count > 0), args), "table kernel");
     PageArgs zero{cache.pool, cache.dims.page_bytes, cache.fresh.pointer, cache.fresh_count};
-    check_hip(launch_zero_pages(cache.stream, zero), "zero pages");
+    check_hip(launch_zero_pages(launch_for(cache, SYNAPSE_KV_KERNEL_PAGES, zero.count > 0), zero), "zero pages");
     PageArgs copy{cache.pool, cache.dims.page_bytes, cache.copies.pointer, cache.copy_count};
-    check_hip(launch_copy_pages(cache.stream, copy), "copy pages");
+    check_hip(launch_copy_pages(launch_for(cache, SYNAPSE_KV_KERNEL_PAGES, copy.count > 0), copy), "copy pages");
     cache.ops.clear();
     cache.fresh_count = 0;
     cache.copy_count = 0;
@@ -335,16 +396,7 @@ Geometry geometry(const SynapseKvCache& cache, uint32_t layer) {
 
 size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1) / alignment * alignment; }
 
-void check_device_pointer(const void* pointer, const char* name) {
-    if (pointer == nullptr) {
-        fail(SYNAPSE_KV_NULL_POINTER, std::string("null pointer: ") + name);
-    }
-    hipPointerAttribute_t attributes{};
-    if (hipPointerGetAttributes(&attributes, pointer) != hipSuccess || attributes.type != hipMemoryTypeDevice) {
-        (void)hipGetLastError();
-        invalid(std::string(name) + " must be device memory");
-    }
-}
+
 
 // Builds and uploads the attention plan of a prepared step.
 //
@@ -595,7 +647,8 @@ void create_cache(const SynapseKvDesc& desc, SynapseKvCache** output) {
         check_hip(hipMemcpy(cache->device_state.pointer, state, sizeof(state), hipMemcpyHostToDevice), "state upload");
         check_hip(hipMemcpy(cache->cosines.pointer, desc.rope_cosines, rope * 4, hipMemcpyHostToDevice), "RoPE upload");
         check_hip(hipMemcpy(cache->sines.pointer, desc.rope_sines, rope * 4, hipMemcpyHostToDevice), "RoPE upload");
-        cache->decode_waves = decode_resident_waves(cache->device, dims.precision == SYNAPSE_KV_F16, dims.head_dim);
+        cache->decode_waves =
+            decode_resident_waves(cache->device, dims.precision == SYNAPSE_KV_F16, dims.head_dim, cache->prefetch != 0);
     } catch (...) {
         delete cache;
         throw;
@@ -699,7 +752,9 @@ void launch_append_layer(SynapseKvCache& cache, uint32_t layer, float* qkv, uint
     args.cosines = cache.cosines.pointer;
     args.sines = cache.sines.pointer;
     args.write_back = write_back ? 1 : 0;
-    check_hip(launch_append(cache.stream, args, cache.step_count, dims.precision == SYNAPSE_KV_F16), "append");
+    check_hip(launch_append(launch_for(cache, SYNAPSE_KV_KERNEL_APPEND, cache.step_count > 0), args, cache.step_count,
+                            dims.precision == SYNAPSE_KV_F16),
+              "append");
 }
 
 // Attention of the prepared step for one layer; with `append`, the step's K/V are appended first (fused into the
@@ -719,8 +774,8 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
         invalid("qkv must be 16-byte aligned");
     }
     set_device(cache);
-    check_device_pointer(qkv, "qkv");
-    check_device_pointer(output, "output");
+    check_device_pointer(cache, qkv, "qkv");
+    check_device_pointer(cache, output, "output");
     // With `append`, qkv stays as the caller wrote it: K is rotated on its way into the pages and Q in registers.
     const bool fused = append && cache.fusable;
     if (append && !fused) {
@@ -746,9 +801,13 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
     args.partial_out = cache.partial_out.pointer;
     args.partial_ml = cache.partial_ml.pointer;
     const bool fp16 = dims.precision == SYNAPSE_KV_F16;
-    check_hip(launch_prefill(cache.stream, args, cache.prefill_items, fp16), "prefill attention");
-    check_hip(launch_decode(cache.stream, args, fp16), "decode attention");
-    check_hip(launch_merge(cache.stream, args, 0, cache.decode_merges + cache.prefill_merges), "split merge");
+    check_hip(launch_prefill(launch_for(cache, SYNAPSE_KV_KERNEL_PREFILL, cache.prefill_items > 0), args,
+                             cache.prefill_items, fp16),
+              "prefill attention");
+    check_hip(launch_decode(launch_for(cache, SYNAPSE_KV_KERNEL_DECODE, args.workers > 0), args, fp16, cache.prefetch != 0),
+              "decode attention");
+    const int merges = cache.decode_merges + cache.prefill_merges;
+    check_hip(launch_merge(launch_for(cache, SYNAPSE_KV_KERNEL_MERGE, merges > 0), args, 0, merges), "split merge");
 }
 
 }  // namespace
@@ -828,6 +887,15 @@ int32_t synapse_kv_set_option(SynapseKvCache* cache, uint32_t option, uint32_t v
             cache->split_keys = value;
         } else if (option == SYNAPSE_KV_OPTION_PREFILL_RUNS) {
             cache->prefill_runs = value != 0 ? 1 : 0;
+        } else if (option == SYNAPSE_KV_OPTION_PROFILE_EVERY) {
+            if (value == 0) {
+                invalid("profile sampling must be at least 1");
+            }
+            cache->profile_every = value;
+        } else if (option == SYNAPSE_KV_OPTION_DECODE_PREFETCH) {
+            cache->prefetch = value != 0 ? 1 : 0;
+            cache->decode_waves = decode_resident_waves(cache->device, cache->dims.precision == SYNAPSE_KV_F16,
+                                                        cache->dims.head_dim, cache->prefetch != 0);
         } else if (option == SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS) {
             if (value == 0 || value % kStepKeys != 0) {
                 invalid("prefill split keys must be a positive multiple of 64");
@@ -958,7 +1026,7 @@ int32_t synapse_kv_append_rope(SynapseKvCache* cache, uint32_t layer, float* qkv
             invalid("qkv_stride is shorter than (heads + 2 * kv_heads) * head_dim");
         }
         set_device(*cache);
-        check_device_pointer(qkv, "qkv");
+        check_device_pointer(*cache, qkv, "qkv");
         launch_append_layer(*cache, layer, qkv, qkv_stride, true);
     });
 }
@@ -977,6 +1045,38 @@ int32_t synapse_kv_append_attention(SynapseKvCache* cache, uint32_t layer, const
         return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache, qkv or output");
     }
     return guarded([&] { run_attention(*cache, layer, qkv, qkv_stride, output, out_stride, true); });
+}
+
+int32_t synapse_kv_profile_begin(SynapseKvCache* cache) {
+    if (cache == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache");
+    }
+    return guarded([&] {
+        cache->profiled.clear();
+        std::fill(std::begin(cache->profile_seen), std::end(cache->profile_seen), 0);
+        cache->profiling = true;
+    });
+}
+
+int32_t synapse_kv_profile_end(SynapseKvCache* cache, SynapseKvProfile* profile) {
+    if (cache == nullptr || profile == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or profile");
+    }
+    return guarded([&] {
+        set_device(*cache);
+        cache->profiling = false;
+        check_hip(hipStreamSynchronize(cache->stream), "synchronize");
+        SynapseKvProfile out{};
+        for (const auto& [kind, index] : cache->profiled) {
+            float milliseconds = 0.0f;
+            const auto& pair = cache->event_pool[index];
+            check_hip(hipEventElapsedTime(&milliseconds, pair.first, pair.second), "profile read");
+            out.launches[kind] += 1;
+            out.milliseconds[kind] += milliseconds;
+        }
+        cache->profiled.clear();
+        *profile = out;
+    });
 }
 
 int32_t synapse_kv_synchronize(SynapseKvCache* cache) {
@@ -1109,7 +1209,7 @@ int32_t synapse_kv_read_kv(SynapseKvCache* cache, uint32_t slot, uint32_t layer,
         args.count = static_cast<int32_t>(count);
         args.keys = staging.pointer;
         args.values = staging.pointer + bytes;
-        hipError_t error = launch_gather(cache->stream, args, dims.precision == SYNAPSE_KV_F16);
+        hipError_t error = launch_gather(launch_for(*cache, SYNAPSE_KV_KERNEL_GATHER, true), args, dims.precision == SYNAPSE_KV_F16);
         if (error == hipSuccess) {
             error = hipStreamSynchronize(cache->stream);
         }

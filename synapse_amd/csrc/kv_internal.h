@@ -8,6 +8,7 @@
 // with 128-bit loads. Elements are float (FP32 KV) or _Float16 (FP16 KV).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -146,17 +147,28 @@ struct GatherArgs {
 
 // Page regions are stored in MFMA-fragment order; see page_layout.h.
 
-// Launchers (each enqueues on `stream` and returns the launch status).
-hipError_t launch_table(hipStream_t stream, const TableArgs& args);
-hipError_t launch_zero_pages(hipStream_t stream, const PageArgs& args);
-hipError_t launch_copy_pages(hipStream_t stream, const PageArgs& args);
-hipError_t launch_append(hipStream_t stream, const AppendArgs& args, int tokens, bool fp16);
-hipError_t launch_decode(hipStream_t stream, const AttentionArgs& args, bool fp16);
-hipError_t launch_merge(hipStream_t stream, const AttentionArgs& args, int first, int count);
+// Where a kernel goes: the cache's stream, and (when profiling) the events its dispatch records at start and end.
+struct Launch {
+    hipStream_t stream;
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+
+// Dispatches `kernel` for `launch` (hipExtLaunchKernelGGL records the events around the dispatch itself).
+#define SYNAPSE_KV_LAUNCH(kernel, grid, block, launch, ...)                                                       \
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, (launch).stream, (launch).start, (launch).stop, 0, __VA_ARGS__)
+
+// Launchers (each enqueues at most one kernel and returns the launch status).
+hipError_t launch_table(const Launch& launch, const TableArgs& args);
+hipError_t launch_zero_pages(const Launch& launch, const PageArgs& args);
+hipError_t launch_copy_pages(const Launch& launch, const PageArgs& args);
+hipError_t launch_append(const Launch& launch, const AppendArgs& args, int tokens, bool fp16);
+hipError_t launch_decode(const Launch& launch, const AttentionArgs& args, bool fp16, bool prefetch);
+hipError_t launch_merge(const Launch& launch, const AttentionArgs& args, int first, int count);
 // Waves of the decode kernel that are resident at once on `device` (the persistent worker count).
-int decode_resident_waves(int device, bool fp16, int head_dim);
-hipError_t launch_prefill(hipStream_t stream, const AttentionArgs& args, int items, bool fp16);
-hipError_t launch_gather(hipStream_t stream, const GatherArgs& args, bool fp16);
+int decode_resident_waves(int device, bool fp16, int head_dim, bool prefetch);
+hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int items, bool fp16);
+hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16);
 
 // Query rows (tokens) per prefill work item: 16 per MFMA column tile, kPrefillTiles tiles per wave.
 constexpr int kPrefillTiles = 2;

@@ -145,27 +145,27 @@ unsigned page_grid(const PageArgs& a) {
 
 }  // namespace
 
-hipError_t launch_table(hipStream_t stream, const TableArgs& args) {
+hipError_t launch_table(const Launch& launch, const TableArgs& args) {
     if (args.op_count == 0) {
         return hipSuccess;
     }
-    hipLaunchKernelGGL(table_kernel, dim3(1), dim3(kTableThreads), 0, stream, args);
+    SYNAPSE_KV_LAUNCH(table_kernel, dim3(1), dim3(kTableThreads), launch, args);
     return hipGetLastError();
 }
 
-hipError_t launch_zero_pages(hipStream_t stream, const PageArgs& args) {
+hipError_t launch_zero_pages(const Launch& launch, const PageArgs& args) {
     if (args.count == 0) {
         return hipSuccess;
     }
-    hipLaunchKernelGGL(zero_pages_kernel, dim3(page_grid(args)), dim3(256), 0, stream, args);
+    SYNAPSE_KV_LAUNCH(zero_pages_kernel, dim3(page_grid(args)), dim3(256), launch, args);
     return hipGetLastError();
 }
 
-hipError_t launch_copy_pages(hipStream_t stream, const PageArgs& args) {
+hipError_t launch_copy_pages(const Launch& launch, const PageArgs& args) {
     if (args.count == 0) {
         return hipSuccess;
     }
-    hipLaunchKernelGGL(copy_pages_kernel, dim3(page_grid(args)), dim3(256), 0, stream, args);
+    SYNAPSE_KV_LAUNCH(copy_pages_kernel, dim3(page_grid(args)), dim3(256), launch, args);
     return hipGetLastError();
 }
 

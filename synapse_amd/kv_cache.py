@@ -33,7 +33,9 @@ from .native import (
     BatchToken,
     CacheDesc,
     NativeKvLibrary,
+    KERNEL_KINDS,
     PageStats,
+    Profile,
 )
 
 PRECISIONS = {"f32": KV_F32, "fp32": KV_F32, "float32": KV_F32, "f16": KV_F16, "fp16": KV_F16, "float16": KV_F16}
@@ -240,6 +242,17 @@ class PagedKvCache:
         self.library.check(
             self.library.c_append_attention(self.handle, layer, _address(qkv), q_stride, _address(output), o_stride)
         )
+
+    def profile_begin(self) -> None:
+        """Starts per-kernel GPU timing (events recorded by each dispatch on the cache's stream)."""
+        self.library.check(self.library.c_profile_begin(self.handle))
+
+    def profile_end(self) -> dict:
+        """Waits for the stream; returns {kind: (launches, milliseconds)} for the kinds that ran."""
+        profile = Profile()
+        self.library.check(self.library.c_profile_end(self.handle, ctypes.byref(profile)))
+        return {kind: (int(profile.launches[index]), float(profile.milliseconds[index]))
+                for index, kind in enumerate(KERNEL_KINDS) if profile.launches[index]}
 
     def synchronize(self) -> None:
         self.library.check(self.library.c_synchronize(self.handle))

@@ -33,6 +33,8 @@ KV_F16 = 1
 OPTION_SPLIT_KEYS = 1
 OPTION_PREFILL_RUNS = 2
 OPTION_PREFILL_SPLIT_KEYS = 3
+OPTION_DECODE_PREFETCH = 4
+OPTION_PROFILE_EVERY = 5
 
 
 class SynapseKvError(RuntimeError):
@@ -108,8 +110,15 @@ class PageStats(ctypes.Structure):
     ]
 
 
+KERNEL_KINDS = ("table", "pages", "append", "decode", "merge", "prefill", "gather")
+
+
+class Profile(ctypes.Structure):
+    _fields_ = [("launches", ctypes.c_uint64 * 8), ("milliseconds", ctypes.c_double * 8)]
+
+
 # Sizes pinned on both sides of the ABI (include/synapse_kv.h static assertions).
-STRUCT_SIZES = {DeviceInfo: 152, BatchToken: 16, CacheDesc: 64, PageStats: 40}
+STRUCT_SIZES = {DeviceInfo: 152, BatchToken: 16, CacheDesc: 64, PageStats: 40, Profile: 128}
 for _struct, _size in STRUCT_SIZES.items():
     assert ctypes.sizeof(_struct) == _size, (_struct.__name__, ctypes.sizeof(_struct))
 
@@ -138,6 +147,8 @@ EXPORTS = {
     "synapse_kv_attention": (_I32, [_P, _U32, _P, _U32, _P, _U32]),
     "synapse_kv_append_attention": (_I32, [_P, _U32, _P, _U32, _P, _U32]),
     "synapse_kv_synchronize": (_I32, [_P]),
+    "synapse_kv_profile_begin": (_I32, [_P]),
+    "synapse_kv_profile_end": (_I32, [_P, ctypes.POINTER(Profile)]),
     "synapse_kv_slot_info": (
         _I32,
         [_P, _U32, ctypes.POINTER(_U32), ctypes.POINTER(_U32), ctypes.POINTER(_U32)],

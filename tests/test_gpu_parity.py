@@ -152,11 +152,15 @@ def test_decode_steps_match_the_restatement(torch_gpu, heads, kv_heads, head_dim
     pair.check_tables()
 
 
+@pytest.mark.parametrize("prefetch", [0, 1])
 @pytest.mark.parametrize("heads,kv_heads,head_dim,precision,page", SHAPES[:4])
-def test_append_attention_matches_the_restatement(torch_gpu, heads, kv_heads, head_dim, precision, page):
-    say("append_attention parity", heads, kv_heads, head_dim, precision, page)
+def test_append_attention_matches_the_restatement(torch_gpu, heads, kv_heads, head_dim, precision, page, prefetch):
+    from synapse_amd.native import OPTION_DECODE_PREFETCH
+
+    say("append_attention parity", heads, kv_heads, head_dim, precision, page, prefetch)
     pair = Pair(torch_gpu, heads=heads, kv_heads=kv_heads, head_dim=head_dim, precision=precision, page=page,
                 growth=max(page, 256), max_pages=96 if page == 64 else 48)
+    pair.gpu.set_option(OPTION_DECODE_PREFETCH, prefetch)
     rng = np.random.default_rng(head_dim + 7)
     lengths = [0, 257, 600]
     for slot, length in enumerate(lengths):
@@ -165,7 +169,11 @@ def test_append_attention_matches_the_restatement(torch_gpu, heads, kv_heads, he
     # Decode steps with one token per slot: one fused launch per layer, split and unsplit rows.
     for split in (256, 64):
         pair.gpu.set_split_keys(split)
+        pair.gpu.profile_begin()
         assert pair.step([(slot, lengths[slot]) for slot in range(3)], rng, fused=True) == 0
+        kernels = pair.gpu.profile_end()
+        assert kernels["decode"][0] == pair.layers and "append" not in kernels
+        assert all(milliseconds > 0 for _, milliseconds in kernels.values())
         lengths = [length + 1 for length in lengths]
     # Two tokens of one slot and a prompt run: the append runs first, then attention, qkv still untouched.
     assert pair.step([(0, lengths[0]), (0, lengths[0] + 5), (1, lengths[1])], rng, fused=True) == 0
