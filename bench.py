@@ -116,9 +116,71 @@ def cpu_baseline(lengths, threads: int) -> dict:
     }
 
 
+def prefill_config(args, torch) -> dict:
+    """Config C5: a 2,048-token chunk attends causally over a 63,488-token FP16 cache plus itself (65,536 keys) in
+    all 28 layers; one timed repetition = the chunk's 28 append_attention calls (append + MFMA prefill + merge)."""
+    from synapse_amd import PagedKvCache
+
+    cached, chunk = 63488, 2048
+    cache = PagedKvCache(layers=LAYERS, heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM, max_positions=65536,
+                         growth_positions=GROWTH, page_tokens=PAGE_TOKENS, precision="f16", session_slots=1,
+                         step_tokens=4096, max_pages=256)
+    cache.set_stream(torch.cuda.current_stream())
+    cache.reserve(0, cached + chunk)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(SEED + 5)
+    width = (HEADS + 2 * KV_HEADS) * HEAD_DIM
+    buffer = torch.empty((4096, width), device="cuda")
+    for first in range(0, cached, 4096):
+        cache.step([(0, p) for p in range(first, first + 4096)])
+        for layer in range(LAYERS):
+            buffer.normal_(generator=generator)
+            cache.append_rope(layer, buffer)
+    qkv = torch.empty((LAYERS, chunk, width), device="cuda").normal_(generator=generator)
+    out = torch.empty((LAYERS, chunk, HEADS * HEAD_DIM), device="cuda")
+    cache.step([(0, cached + j) for j in range(chunk)])
+
+    def run() -> None:
+        for layer in range(LAYERS):
+            cache.append_attention(layer, qkv[layer], out[layer])
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    cache.profile_begin()
+    begin = time.perf_counter()
+    for _ in range(args.steps):
+        run()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - begin
+    kernels = cache.profile_end()
+    cache.close()
+    # Key visits per query head: each chunk token sees the whole cache plus the chunk up to itself.
+    visits = chunk * cached + chunk * (chunk + 1) // 2
+    flops_per_layer = HEADS * visits * 4 * HEAD_DIM
+    seconds = elapsed / args.steps
+    tflops = LAYERS * flops_per_layer / seconds / 1e12
+    prefill_launches, prefill_ms = kernels["prefill"]
+    kernel_tflops = flops_per_layer / (prefill_ms * 1e-3 / prefill_launches) / 1e12
+    return {
+        "metric": "chunked-prefill attention TFLOP/s (MFMA FP16), 7B shape, 2,048-token chunk over 63,488 cached",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(seconds * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": f"synthetic N(0,1) fp32 rows, torch seed {SEED + 5}",
+        "config": {"workload": "C5: 28 layers x (append + causal prefill + split merge), 65,536 keys",
+                   "flops_per_layer": flops_per_layer},
+        "roofline": {"bound": "mfma", "kernel": "prefill_f16_kernel<128>", "achieved": round(kernel_tflops, 2),
+                     "peak": 2500.0, "unit": "TFLOP/s", "frac": round(kernel_tflops / 2500.0, 4), "traffic": None,
+                     "avg_launch_us": round(prefill_ms * 1e3 / prefill_launches, 2),
+                     "kernels_ms": {kind: round(ms, 3) for kind, (count, ms) in kernels.items()}},
+    }
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--config", choices=["c3", "c5"], default="c3",
+                        help="c3: the BASELINE metric (default); c5: chunked-prefill MFMA throughput")
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--split-keys", type=int, default=None)
@@ -141,6 +203,9 @@ def main() -> None:
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a HIP device")
     torch.cuda.set_device(0)
+    if args.config == "c5":
+        print(json.dumps(prefill_config(args, torch)), flush=True)
+        return
     lengths = lengths_for(SEED + CONFIG_OFFSET)
     total_steps = args.warmup + args.steps
     max_positions = int(-(-(int(lengths.max()) + total_steps + 1) // GROWTH) * GROWTH)

@@ -82,7 +82,9 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
         for (int ks = 0; ks < D / 32; ++ks) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                query[c][ks][e] = valid ? static_cast<_Float16>(values[ks][e]) : static_cast<_Float16>(0.0f);
+                // The softmax scale (log2 e / sqrt(d)) is folded into Q before the FP16 conversion.
+                query[c][ks][e] =
+                    valid ? static_cast<_Float16>(values[ks][e] * a.scale_log2) : static_cast<_Float16>(0.0f);
             }
         }
     }
@@ -107,6 +109,7 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
     const int page_tokens = geo.page_tokens;
     // Keys past the block's last token are masked for every column.
     const int key_stop = min(item.key_end, first_position + item.count);
+    const int unmasked_stop = min(item.key_end, first_position + 1);
 
     for (int key0 = item.key_begin; key0 < key_stop; key0 += kStepKeys) {
         const int logical = key0 / page_tokens;
@@ -140,6 +143,8 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
 
         half8 probability[NT][2];
         float alpha[NT];
+        // Steps that end at or before the block's first token (and inside the split) are visible to every column.
+        const bool masked = key0 + kStepKeys > unmasked_stop;
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
             const int column_position = first_position + 16 * c + r;
@@ -148,11 +153,13 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int key = key0 + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
-                    const bool visible = key < item.key_end && key <= column_position;
-                    const float s = visible ? scores[c][t][i] * a.scale_log2 : kNegativeInfinity;
-                    scores[c][t][i] = s;
-                    tile_max = fmaxf(tile_max, s);
+                    if (masked) {
+                        const int key = key0 + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
+                        if (key >= item.key_end || key > column_position) {
+                            scores[c][t][i] = kNegativeInfinity;
+                        }
+                    }
+                    tile_max = fmaxf(tile_max, scores[c][t][i]);
                 }
             }
             tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
