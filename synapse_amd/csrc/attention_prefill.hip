@@ -7,8 +7,9 @@
 // merge with the decode merge kernel (same (max, sum) partial rows).
 //
 // MI355X mapping: one workgroup per (KV head, block of kPrefillTokens tokens, key split) with one wave per query
-// head of the GQA group, so the group's waves read the same K/V lines together. Each wave holds its head's
-// queries for the block as kPrefillTiles MFMA column tiles of 16 tokens and runs the decode kernel's 64-key step:
+// head of the GQA group; the group's waves share every K/V block through a double-buffered LDS stage. Each wave
+// holds its head's queries for the block as kPrefillTiles MFMA column tiles of 16 tokens and runs the decode
+// kernel's 64-key step:
 // S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16, every K/V fragment loaded once and used by all
 // column tiles. Causal masking is a per-element compare against the column's position.
 
@@ -21,6 +22,9 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr float kNegativeInfinity = -__builtin_inff();
+// 16-byte chunks of a staged block each thread carries in registers (a group of at least 4 waves covers the
+// 2,048 chunks of a head_dim 128 block).
+constexpr int kStageLoads = 8;
 
 __device__ inline float fast_exp2(float value) { return __builtin_amdgcn_exp2f(value); }
 
@@ -111,16 +115,60 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
     const int key_stop = min(item.key_end, first_position + item.count);
     const int unmasked_stop = min(item.key_end, first_position + 1);
 
-    for (int key0 = item.key_begin; key0 < key_stop; key0 += kStepKeys) {
+    // The group's waves share each 64-key block through a double-buffered LDS stage: the block's K and V are two
+    // contiguous runs of 16-byte chunks in the page (fragment order), copied with coalesced loads into registers
+    // while the previous block is computed, then into LDS behind one barrier.
+    constexpr int kKeyChunks = kStepKeys * D / 8;
+    constexpr int kBlockChunks = 2 * kKeyChunks;
+    __shared__ half8 stage[2][kBlockChunks];
+    const int threads = blockDim.x;
+    half8 staged[kStageLoads];
+    auto block_source = [&](int key0, int chunk) {
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
         const _Float16* page = reinterpret_cast<const _Float16*>(
             geo.pool + static_cast<uint64_t>(table[logical]) * geo.page_bytes);
-        // Fragment-ordered 64-key blocks (page_layout.h); plain cached loads, since every query block of the run
-        // reads the same keys.
-        const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D) + lane;
-        const half8* values =
-            reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D) + lane;
+        const size_t base = chunk < kKeyChunks ? key_region : value_region;
+        const int offset = chunk < kKeyChunks ? chunk : chunk - kKeyChunks;
+        return reinterpret_cast<const half8*>(page + base + static_cast<size_t>(within) * D) + offset;
+    };
+    auto fetch_block = [&](int key0) {
+#pragma unroll
+        for (int k = 0; k < kStageLoads; ++k) {
+            const int chunk = static_cast<int>(threadIdx.x) + k * threads;
+            if (chunk < kBlockChunks) {
+                staged[k] = *block_source(key0, chunk);
+            }
+        }
+    };
+    auto store_block = [&](int key0, int buffer) {
+#pragma unroll
+        for (int k = 0; k < kStageLoads; ++k) {
+            const int chunk = static_cast<int>(threadIdx.x) + k * threads;
+            if (chunk < kBlockChunks) {
+                stage[buffer][chunk] = staged[k];
+            }
+        }
+        // Groups too small to hold a block in kStageLoads chunks per thread copy the rest directly.
+        for (int chunk = static_cast<int>(threadIdx.x) + kStageLoads * threads; chunk < kBlockChunks; chunk += threads) {
+            stage[buffer][chunk] = *block_source(key0, chunk);
+        }
+    };
+    const int steps = key_stop > item.key_begin ? (key_stop - item.key_begin + kStepKeys - 1) / kStepKeys : 0;
+    if (steps > 0) {
+        fetch_block(item.key_begin);
+        store_block(item.key_begin, 0);
+    }
+    __syncthreads();
+
+    for (int step = 0; step < steps; ++step) {
+        const int key0 = item.key_begin + step * kStepKeys;
+        const bool more = step + 1 < steps;
+        if (more) {
+            fetch_block(key0 + kStepKeys);
+        }
+        const half8* keys = stage[step & 1] + lane;
+        const half8* values = stage[step & 1] + kKeyChunks + lane;
 
         floatx4 scores[NT][4];
 #pragma unroll
@@ -198,6 +246,10 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
                 }
             }
         }
+        if (more) {
+            store_block(key0 + kStepKeys, (step + 1) & 1);
+        }
+        __syncthreads();
     }
 
     const int group = geo.group;
