@@ -13,6 +13,8 @@
 // S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16, every K/V fragment loaded once and used by all
 // column tiles. Causal masking is a per-element compare against the column's position.
 
+#include <type_traits>
+
 #include "kv_internal.h"
 
 namespace synapse_kv {
@@ -20,13 +22,32 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 
 constexpr float kNegativeInfinity = -__builtin_inff();
-// 16-byte chunks of a staged block each thread carries in registers (a group of at least 4 waves covers the
-// 2,048 chunks of a head_dim 128 block).
-constexpr int kStageLoads = 8;
+// Offsets trail the running maximum by less than this (log2 units), so FP16 probabilities stay below 256.
+constexpr float kLazyRescale = 8.0f;
 
 __device__ inline float fast_exp2(float value) { return __builtin_amdgcn_exp2f(value); }
+
+// Cross-lane reductions without LDS. v_permlane16_swap (v_permlane32_swap) of a value with itself returns, in
+// every lane, the value of the lane and of its partner lane ^ 16 (^ 32), one in each result.
+__device__ inline float max_lanes16(float value) {
+    const auto pair = __builtin_amdgcn_permlane16_swap(__float_as_uint(value), __float_as_uint(value), false, false);
+    return fmaxf(__uint_as_float(pair[0]), __uint_as_float(pair[1]));
+}
+__device__ inline float max_lanes32(float value) {
+    const auto pair = __builtin_amdgcn_permlane32_swap(__float_as_uint(value), __float_as_uint(value), false, false);
+    return fmaxf(__uint_as_float(pair[0]), __uint_as_float(pair[1]));
+}
+__device__ inline float sum_lanes16(float value) {
+    const auto pair = __builtin_amdgcn_permlane16_swap(__float_as_uint(value), __float_as_uint(value), false, false);
+    return __uint_as_float(pair[0]) + __uint_as_float(pair[1]);
+}
+__device__ inline float sum_lanes32(float value) {
+    const auto pair = __builtin_amdgcn_permlane32_swap(__float_as_uint(value), __float_as_uint(value), false, false);
+    return __uint_as_float(pair[0]) + __uint_as_float(pair[1]);
+}
 
 // Qwen2RopeTable.Apply (Qwen2CpuState.cs:85-106) for one pair, products and sums rounded separately.
 __device__ inline void rotate_pair(float x, float y, float c, float s, float& first, float& second) {
@@ -93,17 +114,20 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
         }
     }
 
+    // Running state per column tile: O^T accumulators, the column's log2-domain offset (-inf until the column has
+    // seen a key) and the lane's partial sum of probabilities (its 16 keys of each step; lanes g = 0..3 of a
+    // column are added at the end).
     floatx4 out[NT][D / 16];
-    float maximum[NT];
-    float sum[NT];
+    float base[NT];
+    float total[NT];
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt) {
             out[c][mt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        maximum[c] = kNegativeInfinity;
-        sum[c] = 0.0f;
+        base[c] = kNegativeInfinity;
+        total[c] = 0.0f;
     }
 
     const int32_t* table = geo.block_table + static_cast<size_t>(first.slot) * geo.pages_per_slot;
@@ -111,76 +135,65 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
     const size_t key_region = ((static_cast<size_t>(geo.layer) * 2) * geo.kv_heads + item.kv_head) * region;
     const size_t value_region = ((static_cast<size_t>(geo.layer) * 2 + 1) * geo.kv_heads + item.kv_head) * region;
     const int page_tokens = geo.page_tokens;
-    // Keys past the block's last token are masked for every column.
+    // Keys past the block's last token are masked for every column; steps ending at or before the block's first
+    // token (and inside the split) are visible to every column.
     const int key_stop = min(item.key_end, first_position + item.count);
     const int unmasked_stop = min(item.key_end, first_position + 1);
+    const int steps = key_stop > item.key_begin ? (key_stop - item.key_begin + kStepKeys - 1) / kStepKeys : 0;
+    const int clean = unmasked_stop > item.key_begin ? min(steps, (unmasked_stop - item.key_begin) / kStepKeys) : 0;
 
-    // The group's waves share each 64-key block through a double-buffered LDS stage: the block's K and V are two
-    // contiguous runs of 16-byte chunks in the page (fragment order), copied with coalesced loads into registers
-    // while the previous block is computed, then into LDS behind one barrier.
+    // The group's waves share each 64-key block through a 3-deep LDS ring: a block's K and V are two contiguous
+    // runs of 16-byte chunks in its page (fragment order), copied by global_load_lds (each wave instruction moves
+    // 64 chunks, one per lane, into 1 KiB of LDS) two steps ahead of the step that reads its V and one step ahead
+    // of the step that reads its K.
     constexpr int kKeyChunks = kStepKeys * D / 8;
     constexpr int kBlockChunks = 2 * kKeyChunks;
-    __shared__ half8 stage[2][kBlockChunks];
-    const int threads = blockDim.x;
-    half8 staged[kStageLoads];
-    auto block_source = [&](int key0, int chunk) {
-        const int logical = key0 / page_tokens;
-        const int within = key0 - logical * page_tokens;
-        const _Float16* page = reinterpret_cast<const _Float16*>(
-            geo.pool + static_cast<uint64_t>(table[logical]) * geo.page_bytes);
-        const size_t base = chunk < kKeyChunks ? key_region : value_region;
-        const int offset = chunk < kKeyChunks ? chunk : chunk - kKeyChunks;
-        return reinterpret_cast<const half8*>(page + base + static_cast<size_t>(within) * D) + offset;
-    };
-    auto fetch_block = [&](int key0) {
-#pragma unroll
-        for (int k = 0; k < kStageLoads; ++k) {
-            const int chunk = static_cast<int>(threadIdx.x) + k * threads;
-            if (chunk < kBlockChunks) {
-                staged[k] = *block_source(key0, chunk);
-            }
+    constexpr int kBlockSegments = kBlockChunks / 64;
+    __shared__ half8 stage[3][kBlockChunks];
+    const int waves = static_cast<int>(blockDim.x) >> 6;
+    auto page_of = [&](int key0) { return table[key0 / page_tokens]; };
+    // Lane l loads the table entry l pages after the block's (clamped to the slot's table); lane 0's is the
+    // block's page. The per-lane load stays in a vector register until the next step reads lane 0, so the load
+    // is waited for only where it is used.
+    const int last_page = geo.pages_per_slot - 1;
+    auto page_window = [&](int key0) { return table[min(key0 / page_tokens + lane, last_page)]; };
+    auto issue_block = [&](int key0, int page_index, int buffer) {
+        const int within = key0 % page_tokens;
+        const _Float16* page =
+            reinterpret_cast<const _Float16*>(geo.pool + static_cast<uint64_t>(page_index) * geo.page_bytes);
+        const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D);
+        const half8* values = reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D);
+        for (int segment = wave; segment < kBlockSegments; segment += waves) {
+            const int chunk = segment * 64 + lane;
+            const half8* source = chunk < kKeyChunks ? keys + chunk : values + (chunk - kKeyChunks);
+            __builtin_amdgcn_global_load_lds(source, (__attribute__((address_space(3))) void*)(&stage[buffer][segment * 64]),
+                                             16, 0, 0);
         }
     };
-    auto store_block = [&](int key0, int buffer) {
-#pragma unroll
-        for (int k = 0; k < kStageLoads; ++k) {
-            const int chunk = static_cast<int>(threadIdx.x) + k * threads;
-            if (chunk < kBlockChunks) {
-                stage[buffer][chunk] = staged[k];
-            }
-        }
-        // Groups too small to hold a block in kStageLoads chunks per thread copy the rest directly.
-        for (int chunk = static_cast<int>(threadIdx.x) + kStageLoads * threads; chunk < kBlockChunks; chunk += threads) {
-            stage[buffer][chunk] = *block_source(key0, chunk);
-        }
+    // Waits for this wave's outstanding LDS copies (vmcnt 0, other counters untouched), then for the group.
+    auto block_ready = [&]() {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
     };
-    const int steps = key_stop > item.key_begin ? (key_stop - item.key_begin + kStepKeys - 1) / kStepKeys : 0;
-    if (steps > 0) {
-        fetch_block(item.key_begin);
-        store_block(item.key_begin, 0);
-    }
-    __syncthreads();
 
-    for (int step = 0; step < steps; ++step) {
-        const int key0 = item.key_begin + step * kStepKeys;
-        const bool more = step + 1 < steps;
-        if (more) {
-            fetch_block(key0 + kStepKeys);
+    // S^T - offset for one staged block: the accumulators start at -offset of their column, so the scores come out
+    // of the MFMA already relative to the column's offset.
+    auto score_block = [&](const half8* keys, floatx4 (&scores)[NT][4]) {
+        float start[NT];
+#pragma unroll
+        for (int c = 0; c < NT; ++c) {
+            start[c] = base[c] == kNegativeInfinity ? 0.0f : -base[c];
         }
-        const half8* keys = stage[step & 1] + lane;
-        const half8* values = stage[step & 1] + kKeyChunks + lane;
-
-        floatx4 scores[NT][4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             half8 fragment[D / 32];
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
-                fragment[ks] = keys[(t * (D / 32) + ks) * 64];
+                fragment[ks] = keys[(t * (D / 32) + ks) * 64 + lane];
             }
 #pragma unroll
             for (int c = 0; c < NT; ++c) {
-                scores[c][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                scores[c][t] = floatx4{start[c], start[c], start[c], start[c]};
 #pragma unroll
                 for (int ks = 0; ks < D / 32; ++ks) {
                     scores[c][t] =
@@ -188,57 +201,99 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
                 }
             }
         }
+    };
 
-        half8 probability[NT][2];
-        float alpha[NT];
-        // Steps that end at or before the block's first token (and inside the split) are visible to every column.
-        const bool masked = key0 + kStepKeys > unmasked_stop;
+    // The page of the block copied by the next step, loaded a step early so that no step waits on the table.
+    int page_ahead = 0;  // per-lane window, lane 0 used
+    // One step: scores of block `step` are in `current`, the step leaves block step+1's in `upcoming`; block step+1
+    // is staged and block step+2 is copied during the step.
+    auto run_step = [&](int step, auto masked_tag, floatx4(&current)[NT][4], floatx4(&upcoming)[NT][4]) {
+        constexpr bool kMasked = decltype(masked_tag)::value;
+        const int key0 = item.key_begin + step * kStepKeys;
+        if (step + 2 < steps) {
+            issue_block(key0 + 2 * kStepKeys, __builtin_amdgcn_readfirstlane(page_ahead), (step + 2) % 3);
+        }
+        if (step + 3 < steps) {
+            page_ahead = page_window(key0 + 3 * kStepKeys);
+        }
+        // The last step scores a stale buffer too (unused) so that the step has no data-dependent branches.
+        score_block(stage[(step + 1) % 3], upcoming);
+        float tile_max[NT];
+        bool rescale = false;
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
-            const int column_position = first_position + 16 * c + r;
-            float tile_max = kNegativeInfinity;
+            if (kMasked) {
+                const int column_position = first_position + 16 * c + r;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+                for (int t = 0; t < 4; ++t) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (masked) {
+                    for (int i = 0; i < 4; ++i) {
                         const int key = key0 + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
-                        if (key >= item.key_end || key > column_position) {
-                            scores[c][t][i] = kNegativeInfinity;
-                        }
+                        current[c][t][i] =
+                            key >= item.key_end || key > column_position ? kNegativeInfinity : current[c][t][i];
                     }
-                    tile_max = fmaxf(tile_max, scores[c][t][i]);
                 }
             }
-            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
-            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-            const float next = fmaxf(maximum[c], tile_max);
-            // A column may see no key of this split yet; keep its state at (-inf, 0) without NaN.
-            const float base = next == kNegativeInfinity ? 0.0f : next;
-            alpha[c] = fast_exp2(maximum[c] - base);
-            float tile_sum = 0.0f;
+            float m = kNegativeInfinity;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                m = fmaxf(m, fmaxf(fmaxf(current[c][t][0], current[c][t][1]), fmaxf(current[c][t][2], current[c][t][3])));
+            }
+            m = max_lanes32(max_lanes16(m));
+            tile_max[c] = m;
+            // Probabilities relative to a stale offset stay below 2^kLazyRescale; the offset moves only past that
+            // (or when the column sees its first key).
+            rescale |= m > kLazyRescale || (base[c] == kNegativeInfinity && m != kNegativeInfinity);
+        }
+        if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+                const float old_offset = base[c] == kNegativeInfinity ? 0.0f : base[c];
+                const float next = fmaxf(base[c], old_offset + tile_max[c]);
+                const float delta = (next == kNegativeInfinity ? 0.0f : next) - old_offset;
+                const float alpha = base[c] == kNegativeInfinity ? 0.0f : fast_exp2(base[c] - next);
+                base[c] = next;
+                total[c] *= alpha;
+#pragma unroll
+                for (int mt = 0; mt < D / 16; ++mt) {
+                    out[c][mt] *= alpha;
+                }
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    current[c][t] -= delta;
+                    upcoming[c][t] -= delta;
+                }
+            }
+        }
+        half8 probability[NT][2];
+#pragma unroll
+        for (int c = 0; c < NT; ++c) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float p = fast_exp2(scores[c][t][i] - base);
-                    tile_sum += p;
-                    probability[c][t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(p);
+                    probability[c][t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(fast_exp2(current[c][t][i]));
                 }
             }
-            sum[c] = sum[c] * alpha[c] + tile_sum;
-            maximum[c] = next;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    total[c] = __builtin_amdgcn_fdot2(half2{probability[c][h][e], probability[c][h][e + 1]},
+                                                      half2{1.0f16, 1.0f16}, total[c], false);
+                }
+            }
         }
+        const half8* values = stage[step % 3] + kKeyChunks;
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt) {
             half8 value_fragment[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                value_fragment[h] = values[(h * (D / 16) + mt) * 64];
+                value_fragment[h] = values[(h * (D / 16) + mt) * 64 + lane];
             }
 #pragma unroll
             for (int c = 0; c < NT; ++c) {
-                out[c][mt] *= alpha[c];
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     out[c][mt] =
@@ -246,18 +301,53 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
                 }
             }
         }
-        if (more) {
-            store_block(key0 + kStepKeys, (step + 1) & 1);
+        block_ready();
+    };
+    auto advance = [&](floatx4(&current)[NT][4], const floatx4(&upcoming)[NT][4]) {
+#pragma unroll
+        for (int c = 0; c < NT; ++c) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                current[c][t] = upcoming[c][t];
+            }
         }
-        __syncthreads();
+    };
+
+    floatx4 scores_a[NT][4];
+    floatx4 scores_b[NT][4];
+    if (steps > 0) {
+        issue_block(item.key_begin, page_of(item.key_begin), 0);
+        if (steps > 1) {
+            issue_block(item.key_begin + kStepKeys, page_of(item.key_begin + kStepKeys), 1);
+        }
+        if (steps > 2) {
+            page_ahead = page_window(item.key_begin + 2 * kStepKeys);
+        }
+    }
+    block_ready();
+    if (steps > 0) {
+        score_block(stage[0], scores_a);
+    }
+    // Unmasked steps in pairs, the two score sets trading roles; masked steps (at most three) copy instead.
+    int step = 0;
+    for (; step + 1 < clean; step += 2) {
+        run_step(step, std::false_type{}, scores_a, scores_b);
+        run_step(step + 1, std::false_type{}, scores_b, scores_a);
+    }
+    if (step < clean) {
+        run_step(step, std::false_type{}, scores_a, scores_b);
+        advance(scores_a, scores_b);
+        ++step;
+    }
+    for (; step < steps; ++step) {
+        run_step(step, std::true_type{}, scores_a, scores_b);
+        advance(scores_a, scores_b);
     }
 
     const int group = geo.group;
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
-        float total = sum[c];
-        total += __shfl_xor(total, 16);
-        total += __shfl_xor(total, 32);
+        const float sum = sum_lanes32(sum_lanes16(total[c]));
         const int j = 16 * c + r;
         if (j >= item.count) {
             continue;
@@ -265,7 +355,7 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
         const int token = item.first_token + j;
         if (item.row < 0) {
             float* destination = a.output + static_cast<size_t>(token) * a.out_stride + static_cast<size_t>(head) * D;
-            const float inverse = 1.0f / total;
+            const float inverse = 1.0f / sum;
 #pragma unroll
             for (int mt = 0; mt < D / 16; ++mt) {
                 *reinterpret_cast<floatx4*>(destination + 16 * mt + 4 * g) = out[c][mt] * inverse;
@@ -278,8 +368,8 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
                 *reinterpret_cast<floatx4*>(destination + 16 * mt + 4 * g) = out[c][mt];
             }
             if (g == 0) {
-                a.partial_ml[row * 2] = maximum[c];
-                a.partial_ml[row * 2 + 1] = total;
+                a.partial_ml[row * 2] = base[c];
+                a.partial_ml[row * 2 + 1] = sum;
             }
         }
     }
