@@ -7,7 +7,7 @@
 // merge with the decode merge kernel (same (max, sum) partial rows).
 //
 // MI355X mapping: one workgroup per (KV head, block of kPrefillTokens tokens, key split) with one wave per query
-// head of the GQA group; the group's waves share every K/V block through a double-buffered LDS stage. Each wave
+// head of the GQA group; the group's waves share every K/V block through a 4-deep LDS ring. Each wave
 // holds its head's queries for the block as kPrefillTiles MFMA column tiles of 16 tokens and runs the decode
 // kernel's 64-key step:
 // S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16, every K/V fragment loaded once and used by all
@@ -56,12 +56,32 @@ __device__ inline void rotate_pair(float x, float y, float c, float s, float& fi
     second = x * s + y * c;
 }
 
-template <int D>
-__global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
+// s_waitcnt vmcnt(N) with the other counters left alone (expcnt 7, lgkmcnt 15; vmcnt split over bits 3:0 and
+// 15:14).
+template <int N>
+__device__ inline void wait_vector_memory() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// Workgroup barrier after this wave's LDS reads and all but its newest N vector-memory operations (LDS copies)
+// have completed. __syncthreads would also wait for every outstanding copy (its workgroup fence waits for
+// vmcnt 0); the compiler-level memory clobbers keep LDS accesses on their side of the barrier.
+template <int N>
+__device__ inline void barrier_after_copies() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int D, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a) {
     constexpr int NT = kPrefillTiles;
     const PrefillItem item = a.prefill[blockIdx.x];
     const Geometry& geo = a.geo;
-    const int wave = threadIdx.x >> 6;  // query head within the group
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // query head within the group
     const int lane = threadIdx.x & 63;
     const int r = lane & 15;
     const int g = lane >> 4;
@@ -142,38 +162,64 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
     const int steps = key_stop > item.key_begin ? (key_stop - item.key_begin + kStepKeys - 1) / kStepKeys : 0;
     const int clean = unmasked_stop > item.key_begin ? min(steps, (unmasked_stop - item.key_begin) / kStepKeys) : 0;
 
-    // The group's waves share each 64-key block through a 3-deep LDS ring: a block's K and V are two contiguous
-    // runs of 16-byte chunks in its page (fragment order), copied by global_load_lds (each wave instruction moves
-    // 64 chunks, one per lane, into 1 KiB of LDS) two steps ahead of the step that reads its V and one step ahead
-    // of the step that reads its K.
+    // The group's waves share each 64-key block through a 4-deep LDS ring. A block's K and V are two contiguous
+    // runs of 16-byte chunks in its page (fragment order); global_load_lds moves 64 of them per wave instruction,
+    // one per lane, into 1 KiB of LDS. Block b is copied during step b - 3 and completes by the end of step b - 2
+    // (its K is read in step b - 1, its V in step b), so every copy has two steps to land.
     constexpr int kKeyChunks = kStepKeys * D / 8;
     constexpr int kBlockChunks = 2 * kKeyChunks;
     constexpr int kBlockSegments = kBlockChunks / 64;
-    __shared__ half8 stage[3][kBlockChunks];
-    const int waves = static_cast<int>(blockDim.x) >> 6;
-    auto page_of = [&](int key0) { return table[key0 / page_tokens]; };
-    // Lane l loads the table entry l pages after the block's (clamped to the slot's table); lane 0's is the
-    // block's page. The per-lane load stays in a vector register until the next step reads lane 0, so the load
-    // is waited for only where it is used.
+    constexpr int kKeySegments = kKeyChunks / 64;
+    constexpr int kRing = 4;
+    constexpr int kLoads = (kBlockSegments + WAVES - 1) / WAVES;
+    __shared__ half8 stage[kRing][kBlockChunks];
+    // This wave copies segments wave, wave + WAVES, ...: kLoads of them, or kLoads - 1.
+    const bool full_share = wave + (kLoads - 1) * WAVES < kBlockSegments;
+
+    // Page numbers of 64 consecutive logical pages, one per lane, read with v_readlane and reloaded only when the
+    // copy position leaves the window, so the copies never wait on a table load.
     const int last_page = geo.pages_per_slot - 1;
-    auto page_window = [&](int key0) { return table[min(key0 / page_tokens + lane, last_page)]; };
-    auto issue_block = [&](int key0, int page_index, int buffer) {
-        const int within = key0 % page_tokens;
-        const _Float16* page =
-            reinterpret_cast<const _Float16*>(geo.pool + static_cast<uint64_t>(page_index) * geo.page_bytes);
-        const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D);
-        const half8* values = reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D);
-        for (int segment = wave; segment < kBlockSegments; segment += waves) {
-            const int chunk = segment * 64 + lane;
-            const half8* source = chunk < kKeyChunks ? keys + chunk : values + (chunk - kKeyChunks);
-            __builtin_amdgcn_global_load_lds(source, (__attribute__((address_space(3))) void*)(&stage[buffer][segment * 64]),
-                                             16, 0, 0);
+    int copy_logical = item.key_begin / page_tokens;
+    int copy_within = item.key_begin - copy_logical * page_tokens;
+    int window_first = copy_logical;
+    int window = table[min(window_first + lane, last_page)];
+    auto issue_next_block = [&](int buffer) {
+        if (copy_logical - window_first >= 64) {
+            window_first = copy_logical;
+            window = table[min(window_first + lane, last_page)];
+            wait_vector_memory<0>();
+        }
+        const int page_index = __builtin_amdgcn_readlane(window, copy_logical - window_first);
+        const uint8_t* page = geo.pool + static_cast<uint64_t>(page_index) * geo.page_bytes;
+        const uint8_t* keys = page + (key_region + static_cast<size_t>(copy_within) * D) * sizeof(_Float16);
+        const uint8_t* values = page + (value_region + static_cast<size_t>(copy_within) * D) * sizeof(_Float16);
+#pragma unroll
+        for (int k = 0; k < kLoads; ++k) {
+            const int segment = wave + k * WAVES;
+            if (segment < kBlockSegments) {
+                const uint8_t* source =
+                    (segment < kKeySegments ? keys + segment * 1024 : values + (segment - kKeySegments) * 1024) +
+                    lane * 16;
+                __builtin_amdgcn_global_load_lds(
+                    source, (__attribute__((address_space(3))) void*)(&stage[buffer][segment * 64]), 16, 0, 0);
+            }
+        }
+        copy_within += kStepKeys;
+        if (copy_within == page_tokens) {
+            copy_within = 0;
+            ++copy_logical;
         }
     };
-    // Waits for this wave's outstanding LDS copies (vmcnt 0, other counters untouched), then for the group.
-    auto block_ready = [&]() {
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-        __syncthreads();
+    // Waits for this wave's copies, except the newest block's when `newest_in_flight`, then for the group (whose
+    // waves have then finished reading the buffer the next copy overwrites).
+    auto blocks_ready = [&](bool newest_in_flight) {
+        if (!newest_in_flight) {
+            barrier_after_copies<0>();
+        } else if (full_share) {
+            barrier_after_copies<kLoads>();
+        } else {
+            barrier_after_copies<kLoads - 1>();
+        }
     };
 
     // S^T - offset for one staged block: the accumulators start at -offset of their column, so the scores come out
@@ -203,21 +249,17 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
         }
     };
 
-    // The page of the block copied by the next step, loaded a step early so that no step waits on the table.
-    int page_ahead = 0;  // per-lane window, lane 0 used
-    // One step: scores of block `step` are in `current`, the step leaves block step+1's in `upcoming`; block step+1
-    // is staged and block step+2 is copied during the step.
+    // One step: scores of block `step` are in `current`, the step leaves block step+1's in `upcoming`; blocks step
+    // and step+1 are staged, step+2 may be in flight and step+3 is copied during the step.
     auto run_step = [&](int step, auto masked_tag, floatx4(&current)[NT][4], floatx4(&upcoming)[NT][4]) {
         constexpr bool kMasked = decltype(masked_tag)::value;
         const int key0 = item.key_begin + step * kStepKeys;
-        if (step + 2 < steps) {
-            issue_block(key0 + 2 * kStepKeys, __builtin_amdgcn_readfirstlane(page_ahead), (step + 2) % 3);
-        }
-        if (step + 3 < steps) {
-            page_ahead = page_window(key0 + 3 * kStepKeys);
+        const bool copying = step + 3 < steps;
+        if (copying) {
+            issue_next_block((step + 3) % kRing);
         }
         // The last step scores a stale buffer too (unused) so that the step has no data-dependent branches.
-        score_block(stage[(step + 1) % 3], upcoming);
+        score_block(stage[(step + 1) % kRing], upcoming);
         float tile_max[NT];
         bool rescale = false;
 #pragma unroll
@@ -284,7 +326,7 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
                 }
             }
         }
-        const half8* values = stage[step % 3] + kKeyChunks;
+        const half8* values = stage[step % kRing] + kKeyChunks;
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt) {
             half8 value_fragment[2];
@@ -301,7 +343,7 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
                 }
             }
         }
-        block_ready();
+        blocks_ready(copying);
     };
     auto advance = [&](floatx4(&current)[NT][4], const floatx4(&upcoming)[NT][4]) {
 #pragma unroll
@@ -315,16 +357,10 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
 
     floatx4 scores_a[NT][4];
     floatx4 scores_b[NT][4];
-    if (steps > 0) {
-        issue_block(item.key_begin, page_of(item.key_begin), 0);
-        if (steps > 1) {
-            issue_block(item.key_begin + kStepKeys, page_of(item.key_begin + kStepKeys), 1);
-        }
-        if (steps > 2) {
-            page_ahead = page_window(item.key_begin + 2 * kStepKeys);
-        }
+    for (int block = 0; block < min(steps, kRing - 1); ++block) {
+        issue_next_block(block);
     }
-    block_ready();
+    blocks_ready(false);
     if (steps > 0) {
         score_block(stage[0], scores_a);
     }
@@ -375,6 +411,16 @@ __global__ __launch_bounds__(512) void prefill_f16_kernel(AttentionArgs a) {
     }
 }
 
+template <int WAVES>
+hipError_t launch_prefill_for(const Launch& launch, const AttentionArgs& args, dim3 grid, dim3 block) {
+    if (args.geo.head_dim == 128) {
+        SYNAPSE_KV_LAUNCH((prefill_f16_kernel<128, WAVES>), grid, block, launch, args);
+    } else {
+        SYNAPSE_KV_LAUNCH((prefill_f16_kernel<64, WAVES>), grid, block, launch, args);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int items, bool fp16) {
@@ -386,12 +432,18 @@ hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int i
     }
     const dim3 grid(items);
     const dim3 block(args.geo.group * 64);
-    if (args.geo.head_dim == 128) {
-        SYNAPSE_KV_LAUNCH(prefill_f16_kernel<128>, grid, block, launch, args);
-    } else {
-        SYNAPSE_KV_LAUNCH(prefill_f16_kernel<64>, grid, block, launch, args);
+    // One wave per query head of the group (validated at cache creation: 1..8).
+    switch (args.geo.group) {
+        case 1: return launch_prefill_for<1>(launch, args, grid, block);
+        case 2: return launch_prefill_for<2>(launch, args, grid, block);
+        case 3: return launch_prefill_for<3>(launch, args, grid, block);
+        case 4: return launch_prefill_for<4>(launch, args, grid, block);
+        case 5: return launch_prefill_for<5>(launch, args, grid, block);
+        case 6: return launch_prefill_for<6>(launch, args, grid, block);
+        case 7: return launch_prefill_for<7>(launch, args, grid, block);
+        case 8: return launch_prefill_for<8>(launch, args, grid, block);
+        default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace synapse_kv
