@@ -183,7 +183,7 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
     int copy_within = item.key_begin - copy_logical * page_tokens;
     int window_first = copy_logical;
     int window = table[min(window_first + lane, last_page)];
-    auto issue_next_block = [&](int buffer) {
+    auto issue_next_block = [&](int buffer) __attribute__((always_inline)) {
         if (copy_logical - window_first >= 64) {
             window_first = copy_logical;
             window = table[min(window_first + lane, last_page)];
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
     };
     // Waits for this wave's copies, except the newest block's when `newest_in_flight`, then for the group (whose
     // waves have then finished reading the buffer the next copy overwrites).
-    auto blocks_ready = [&](bool newest_in_flight) {
+    auto blocks_ready = [&](bool newest_in_flight) __attribute__((always_inline)) {
         if (!newest_in_flight) {
             barrier_after_copies<0>();
         } else if (full_share) {
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
 
     // S^T - offset for one staged block: the accumulators start at -offset of their column, so the scores come out
     // of the MFMA already relative to the column's offset.
-    auto score_block = [&](const half8* keys, floatx4 (&scores)[NT][4]) {
+    auto score_block = [&](const half8* keys, floatx4 (&scores)[NT][4]) __attribute__((always_inline)) {
         float start[NT];
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
@@ -249,15 +249,12 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
         }
     };
 
-    // One step: scores of block `step` are in `current`, the step leaves block step+1's in `upcoming`; blocks step
-    // and step+1 are staged, step+2 may be in flight and step+3 is copied during the step.
-    auto run_step = [&](int step, auto masked_tag, floatx4(&current)[NT][4], floatx4(&upcoming)[NT][4]) {
+    // Softmax half of a step: scores of block `step` are in `current`; it leaves block step+1's in `upcoming` and
+    // the step's FP16 probabilities in `probability`.
+    half8 probability[NT][2];
+    auto softmax_phase = [&](int step, auto masked_tag, floatx4(&current)[NT][4], floatx4(&upcoming)[NT][4]) __attribute__((always_inline)) {
         constexpr bool kMasked = decltype(masked_tag)::value;
         const int key0 = item.key_begin + step * kStepKeys;
-        const bool copying = step + 3 < steps;
-        if (copying) {
-            issue_next_block((step + 3) % kRing);
-        }
         // The last step scores a stale buffer too (unused) so that the step has no data-dependent branches.
         score_block(stage[(step + 1) % kRing], upcoming);
         float tile_max[NT];
@@ -307,7 +304,6 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
                 }
             }
         }
-        half8 probability[NT][2];
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
 #pragma unroll
@@ -326,6 +322,9 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
                 }
             }
         }
+    };
+    // PV half of a step: O^T += V^T P^T for block `step` with the probabilities the step's softmax left.
+    auto pv_phase = [&](int step) __attribute__((always_inline)) {
         const half8* values = stage[step % kRing] + kKeyChunks;
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt) {
@@ -343,9 +342,37 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
                 }
             }
         }
+    };
+    // Two barriers per step. Waves 0-3 (one per SIMD) run softmax then PV of each step; the waves sharing a SIMD
+    // with them (4-7) run half a step behind: PV of the previous step, then the softmax. Each SIMD then has one
+    // wave in the MFMA-only PV half while the other is in the VALU-heavy softmax half. In the first half of step i
+    // the group reads K(i+1) and V(i-1), in the second K(i+1) and V(i); block i+3 is copied in the second half,
+    // into the buffer V(i-1) held.
+    auto run_step = [&](int step, auto late_tag, auto masked_tag, floatx4(&current)[NT][4],
+                        floatx4(&upcoming)[NT][4]) __attribute__((always_inline)) {
+        constexpr bool kLate = decltype(late_tag)::value;
+        const bool copying = step + 3 < steps;
+        if (kLate) {
+            if (step > 0) {
+                pv_phase(step - 1);
+            }
+        } else {
+            softmax_phase(step, masked_tag, current, upcoming);
+        }
+        if (WAVES > 4) {
+            barrier_after_copies<63>();
+        }
+        if (copying) {
+            issue_next_block((step + 3) % kRing);
+        }
+        if (kLate) {
+            softmax_phase(step, masked_tag, current, upcoming);
+        } else {
+            pv_phase(step);
+        }
         blocks_ready(copying);
     };
-    auto advance = [&](floatx4(&current)[NT][4], const floatx4(&upcoming)[NT][4]) {
+    auto advance = [&](floatx4(&current)[NT][4], const floatx4(&upcoming)[NT][4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
 #pragma unroll
@@ -364,20 +391,30 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
     if (steps > 0) {
         score_block(stage[0], scores_a);
     }
-    // Unmasked steps in pairs, the two score sets trading roles; masked steps (at most three) copy instead.
-    int step = 0;
-    for (; step + 1 < clean; step += 2) {
-        run_step(step, std::false_type{}, scores_a, scores_b);
-        run_step(step + 1, std::false_type{}, scores_b, scores_a);
-    }
-    if (step < clean) {
-        run_step(step, std::false_type{}, scores_a, scores_b);
-        advance(scores_a, scores_b);
-        ++step;
-    }
-    for (; step < steps; ++step) {
-        run_step(step, std::true_type{}, scores_a, scores_b);
-        advance(scores_a, scores_b);
+    auto run_steps = [&](auto late_tag) __attribute__((always_inline)) {
+        // Unmasked steps in pairs, the two score sets trading roles; masked steps (at most three) copy instead.
+        int step = 0;
+        for (; step + 1 < clean; step += 2) {
+            run_step(step, late_tag, std::false_type{}, scores_a, scores_b);
+            run_step(step + 1, late_tag, std::false_type{}, scores_b, scores_a);
+        }
+        if (step < clean) {
+            run_step(step, late_tag, std::false_type{}, scores_a, scores_b);
+            advance(scores_a, scores_b);
+            ++step;
+        }
+        for (; step < steps; ++step) {
+            run_step(step, late_tag, std::true_type{}, scores_a, scores_b);
+            advance(scores_a, scores_b);
+        }
+        if (decltype(late_tag)::value && steps > 0) {
+            pv_phase(steps - 1);
+        }
+    };
+    if (WAVES > 4 && wave >= 4) {
+        run_steps(std::true_type{});
+    } else {
+        run_steps(std::false_type{});
     }
 
     const int group = geo.group;
