@@ -255,6 +255,8 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
     auto softmax_phase = [&](int step, auto masked_tag, floatx4(&current)[NT][4], floatx4(&upcoming)[NT][4]) __attribute__((always_inline)) {
         constexpr bool kMasked = decltype(masked_tag)::value;
         const int key0 = item.key_begin + step * kStepKeys;
+        // The VALU-heavy half issues ahead of the SIMD's other wave, whose PV MFMAs fill the matrix pipe meanwhile.
+        __builtin_amdgcn_s_setprio(1);
         // The last step scores a stale buffer too (unused) so that the step has no data-dependent branches.
         score_block(stage[(step + 1) % kRing], upcoming);
         float tile_max[NT];
@@ -322,6 +324,7 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
                 }
             }
         }
+        __builtin_amdgcn_s_setprio(0);
     };
     // PV half of a step: O^T += V^T P^T for block `step` with the probabilities the step's softmax left.
     auto pv_phase = [&](int step) __attribute__((always_inline)) {
