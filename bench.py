@@ -126,6 +126,8 @@ def prefill_config(args, torch) -> dict:
                          growth_positions=GROWTH, page_tokens=PAGE_TOKENS, precision="f16", session_slots=1,
                          step_tokens=4096, max_pages=256)
     cache.set_stream(torch.cuda.current_stream())
+    if args.prefill_split_keys:
+        cache.set_prefill_split_keys(args.prefill_split_keys)
     cache.reserve(0, cached + chunk)
     generator = torch.Generator(device="cuda")
     generator.manual_seed(SEED + 5)
@@ -167,7 +169,7 @@ def prefill_config(args, torch) -> dict:
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(seconds * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": f"synthetic N(0,1) fp32 rows, torch seed {SEED + 5}",
-        "config": {"workload": "C5: 28 layers x (append + causal prefill + split merge), 65,536 keys",
+        "config": {"workload": "C5: 28 layers x (append + causal prefill, split-K merge when planned), 65,536 keys",
                    "flops_per_layer": flops_per_layer},
         "roofline": {"bound": "mfma", "kernel": "prefill_f16_kernel<128>", "achieved": round(kernel_tflops, 2),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(kernel_tflops / 2500.0, 4), "traffic": None,
@@ -184,6 +186,7 @@ def main() -> None:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--split-keys", type=int, default=None)
+    parser.add_argument("--prefill-split-keys", type=int, default=None, help="c5: keys per prefill work item")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--prefetch", type=int, default=None, help="decode kernel variant (0 or 1)")
     parser.add_argument("--separate", action="store_true",

@@ -42,7 +42,7 @@ extern "C" {
 /* Tuning options for synapse_kv_set_option. */
 #define SYNAPSE_KV_OPTION_SPLIT_KEYS 1u     /* fewest keys per decode wave worker; a multiple of 64 (default 256) */
 #define SYNAPSE_KV_OPTION_PREFILL_RUNS 2u   /* 1: FP16 prompt runs use the MFMA prefill kernel (default); 0: decode path */
-#define SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS 3u /* keys per prefill split-K work item; a multiple of 64 (default 16384) */
+#define SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS 3u /* keys per prefill split-K work item, a multiple of 64; 0 (default): fill the device */
 #define SYNAPSE_KV_OPTION_DECODE_PREFETCH 4u /* 1: FP16 decode keeps the next step's loads in flight (two register sets) */
 #define SYNAPSE_KV_OPTION_PROFILE_EVERY 5u   /* profile mode times every n-th launch of each kernel kind (default 1) */
 

@@ -461,7 +461,39 @@ hipError_t launch_prefill_for(const Launch& launch, const AttentionArgs& args, d
     return hipGetLastError();
 }
 
+template <int D>
+int prefill_blocks_per_cu(int group) {
+    int blocks = 0;
+    hipError_t status = hipErrorInvalidValue;
+    switch (group) {
+        case 1: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 1>, 64, 0); break;
+        case 2: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 2>, 128, 0); break;
+        case 3: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 3>, 192, 0); break;
+        case 4: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 4>, 256, 0); break;
+        case 5: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 5>, 320, 0); break;
+        case 6: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 6>, 384, 0); break;
+        case 7: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 7>, 448, 0); break;
+        case 8: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 8>, 512, 0); break;
+        default: break;
+    }
+    if (status != hipSuccess) {
+        (void)hipGetLastError();
+        return 1;
+    }
+    return blocks > 0 ? blocks : 1;
+}
+
 }  // namespace
+
+int prefill_resident_blocks(int device, int head_dim, int group) {
+    hipDeviceProp_t properties{};
+    if (hipGetDeviceProperties(&properties, device) != hipSuccess) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    const int per_cu = head_dim == 128 ? prefill_blocks_per_cu<128>(group) : prefill_blocks_per_cu<64>(group);
+    return properties.multiProcessorCount * per_cu;
+}
 
 hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int items, bool fp16) {
     if (items == 0) {

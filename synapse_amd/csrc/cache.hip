@@ -177,7 +177,8 @@ struct SynapseKvCache {
     hipStream_t stream = nullptr;
     uint32_t split_keys = 256;  // fewest keys per decode wave worker
     uint32_t prefill_runs = 1;
-    uint32_t prefill_split_keys = 16384;
+    uint32_t prefill_split_keys = 0;     // 0: chosen per step (plan_step)
+    int32_t prefill_slots = 256;         // resident prefill workgroups on the device
     uint32_t prefetch = 1;  // decode kernel variant: 1 = two register sets, next step's loads in flight
 
     // Host shadow of the allocator (same rules as the table kernel).
@@ -398,6 +399,50 @@ size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1)
 
 
 
+// Automatic prefill split: the piece length (in 64-key steps) with the shortest estimated makespan when the
+// pieces are spread over the device's resident workgroup slots. Candidates cut the longest block into 1..32
+// pieces; a candidate's estimate is the smaller of (rounds of slots) x piece and (average load per slot + one
+// piece), the second bounding greedy scheduling of uneven pieces. Splitting further must gain 5%, since every
+// split adds partial rows and a merge.
+int64_t choose_prefill_chunk(const SynapseKvCache& cache, const SynapseKvBatchToken* tokens,
+                             const std::vector<std::pair<int32_t, int32_t>>& runs) {
+    std::vector<int64_t> blocks;
+    for (const auto& [run_start, run_end] : runs) {
+        for (int32_t first = run_start; first < run_end; first += kPrefillTokens) {
+            const int32_t size = std::min<int32_t>(kPrefillTokens, run_end - first);
+            blocks.push_back((tokens[first + size - 1].position + kStepKeys) / kStepKeys);
+        }
+    }
+    const int64_t heads = cache.dims.kv_heads;
+    const int64_t slots = std::max<int32_t>(1, cache.prefill_slots);
+    const int64_t longest = *std::max_element(blocks.begin(), blocks.end());
+    int64_t total = 0;
+    for (int64_t steps : blocks) {
+        total += steps * heads;
+    }
+    const int64_t fewest = kMinPrefillChunk / kStepKeys;
+    int64_t best_chunk = longest;
+    double best_estimate = 0.0;
+    for (int64_t pieces = 1; pieces <= 32; ++pieces) {
+        const int64_t chunk = (longest + pieces - 1) / pieces;
+        if (pieces > 1 && chunk < fewest) {
+            break;
+        }
+        int64_t items = 0;
+        for (int64_t steps : blocks) {
+            items += (steps + chunk - 1) / chunk * heads;
+        }
+        const double rounds = static_cast<double>((items + slots - 1) / slots) * chunk;
+        const double greedy = static_cast<double>(total) / slots + chunk;
+        const double estimate = std::min(rounds, greedy);
+        if (pieces == 1 || estimate < 0.95 * best_estimate) {
+            best_estimate = estimate;
+            best_chunk = chunk;
+        }
+    }
+    return best_chunk;
+}
+
 // Builds and uploads the attention plan of a prepared step.
 //
 // Lone tokens (and prompt runs of FP32 caches) go to the decode kernel: every (token, KV head) row is cut into
@@ -405,7 +450,9 @@ size_t align_up(size_t value, size_t alignment) { return (value + alignment - 1)
 // wave streams the same number of K/V bytes whatever the ragged lengths. Rows cut by a worker boundary get partial
 // rows and a merge entry. FP16 prompt runs (plan_attention, schedule.rs:34-86: consecutive tokens of one slot at
 // consecutive positions) go to the MFMA prefill kernel in blocks of kPrefillTokens tokens per KV head, their keys
-// split every prefill_split_keys keys and merged by the merge kernel.
+// split into work items of at most `chunk` keys whose partial rows the merge kernel combines. The chunk is the
+// prefill_split_keys option when set, otherwise chosen by choose_prefill_chunk: runs that already fill the device
+// are not split (and need no merge), short chunks over long caches are.
 void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t count) {
     const Dims& dims = cache.dims;
     struct Row {
@@ -490,13 +537,18 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         }
     }
 
-    // Prefill blocks.
+    // Prefill blocks. A block's keys are cut into the fewest pieces of at most `chunk_steps` 64-key steps, of
+    // (nearly) equal length.
+    int64_t chunk_steps = cache.prefill_split_keys / kStepKeys;
+    if (chunk_steps == 0 && !runs.empty()) {
+        chunk_steps = choose_prefill_chunk(cache, tokens, runs);
+    }
     for (const auto& [run_start, run_end] : runs) {
         for (int32_t first = run_start; first < run_end; first += kPrefillTokens) {
             const int32_t size = std::min<int32_t>(kPrefillTokens, run_end - first);
             const int32_t keys = tokens[first + size - 1].position + 1;
-            const int32_t chunk = static_cast<int32_t>(cache.prefill_split_keys);
-            const int32_t splits = (keys + chunk - 1) / chunk;
+            const int64_t steps = (keys + kStepKeys - 1) / kStepKeys;
+            const int32_t splits = static_cast<int32_t>((steps + chunk_steps - 1) / chunk_steps);
             const int32_t stride = static_cast<int32_t>(dims.kv_heads) * splits;
             if (splits > 1) {
                 for (int32_t j = 0; j < size; ++j) {
@@ -510,8 +562,9 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             }
             for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
                 for (int32_t part = 0; part < splits; ++part) {
-                    const int32_t begin = part * chunk;
-                    const int32_t finish = std::min(keys, begin + chunk);
+                    const int32_t begin = static_cast<int32_t>(part * steps / splits * kStepKeys);
+                    const int32_t finish =
+                        std::min<int32_t>(keys, static_cast<int32_t>((part + 1) * steps / splits * kStepKeys));
                     const int32_t row = splits > 1 ? partial_rows + static_cast<int32_t>(kv_head) * splits + part : -1;
                     prefill.push_back(PrefillItem{first, size, static_cast<int32_t>(kv_head), begin, finish, row,
                                                   stride, 0});
@@ -649,6 +702,8 @@ void create_cache(const SynapseKvDesc& desc, SynapseKvCache** output) {
         check_hip(hipMemcpy(cache->sines.pointer, desc.rope_sines, rope * 4, hipMemcpyHostToDevice), "RoPE upload");
         cache->decode_waves =
             decode_resident_waves(cache->device, dims.precision == SYNAPSE_KV_F16, dims.head_dim, cache->prefetch != 0);
+        cache->prefill_slots =
+            prefill_resident_blocks(cache->device, static_cast<int>(dims.head_dim), static_cast<int>(dims.heads / dims.kv_heads));
     } catch (...) {
         delete cache;
         throw;
@@ -897,8 +952,8 @@ int32_t synapse_kv_set_option(SynapseKvCache* cache, uint32_t option, uint32_t v
             cache->decode_waves = decode_resident_waves(cache->device, cache->dims.precision == SYNAPSE_KV_F16,
                                                         cache->dims.head_dim, cache->prefetch != 0);
         } else if (option == SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS) {
-            if (value == 0 || value % kStepKeys != 0) {
-                invalid("prefill split keys must be a positive multiple of 64");
+            if (value % kStepKeys != 0) {
+                invalid("prefill split keys must be 0 (automatic) or a multiple of 64");
             }
             cache->prefill_split_keys = value;
         } else {

@@ -167,6 +167,8 @@ hipError_t launch_decode(const Launch& launch, const AttentionArgs& args, bool f
 hipError_t launch_merge(const Launch& launch, const AttentionArgs& args, int first, int count);
 // Waves of the decode kernel that are resident at once on `device` (the persistent worker count).
 int decode_resident_waves(int device, bool fp16, int head_dim, bool prefetch);
+// Prefill workgroups resident on the whole device at once (occupancy of the group's kernel times the CU count).
+int prefill_resident_blocks(int device, int head_dim, int group);
 hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int items, bool fp16);
 hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16);
 
@@ -175,5 +177,7 @@ constexpr int kPrefillTiles = 2;
 constexpr int kPrefillTokens = 16 * kPrefillTiles;
 // Keys per decode/prefill inner step.
 constexpr int kStepKeys = 64;
+// Fewest keys per prefill work item when the split is chosen automatically.
+constexpr int kMinPrefillChunk = 1024;
 
 }  // namespace synapse_kv

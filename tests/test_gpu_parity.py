@@ -56,9 +56,10 @@ class Pair:
         assert status == expected, (name, args, status, expected)
         return status
 
-    def step(self, tokens, rng, attend=True, fused=False):
+    def step(self, tokens, rng, attend=True, fused=False, key_scale=None):
         """One step: prepare, then per layer append (+ attention); checks every output. `fused` drives the layer
-        through append_attention (qkv stays unrotated) instead of append_rope + attention."""
+        through append_attention (qkv stays unrotated) instead of append_rope + attention. `key_scale(position)`
+        multiplies each token's K row (rising scales move the running maximum often)."""
         torch = self.torch
         status = self.call("step", tokens)
         if status:
@@ -66,6 +67,10 @@ class Pair:
         count = len(tokens)
         for layer in range(self.layers):
             rows = rng.standard_normal((count, self.width)).astype(np.float32)
+            if key_scale is not None:
+                k0, k1 = self.heads * self.head_dim, (self.heads + self.kv_heads) * self.head_dim
+                scales = np.array([key_scale(position) for _, position in tokens], dtype=np.float32)
+                rows[:, k0:k1] *= scales[:, None]
             qkv = torch.from_numpy(rows.copy()).cuda()
             original = rows.copy()
             out = torch.full((count, self.heads * self.head_dim), float("nan"), device="cuda")
@@ -210,9 +215,26 @@ def test_prompt_runs_match_the_restatement(torch_gpu, head_dim):
     assert pair.step([(0, p) for p in range(233, 300)] + [(1, p) for p in range(0, 45)], rng) == 0
     pair.gpu.set_prefill_split_keys(16384)
     assert pair.step([(1, 45), (0, 300)] + [(2, p) for p in range(0, 31)], rng) == 0
+    pair.gpu.set_prefill_split_keys(0)  # automatic: split to fill the device
+    assert pair.step([(2, p) for p in range(31, 97)] + [(3, p) for p in range(0, 64)], rng) == 0
     pair.check_tables()
-    for slot in range(3):
+    for slot in range(4):
         pair.check_contents(slot)
+
+
+@pytest.mark.parametrize("split", [0, 64, 256])
+def test_prefill_running_maximum_moves_often(torch_gpu, split):
+    """Keys whose scale rises with position push every column's maximum up many times, through the lazy offset
+    update (threshold crossings, the first key of a column, split partial rows merged afterwards)."""
+    say("prefill rising scores", split)
+    pair = Pair(torch_gpu, heads=28, kv_heads=4, head_dim=128, max_pages=64, layers=1)
+    rng = np.random.default_rng(40 + split)
+    pair.gpu.set_prefill_split_keys(split)
+    rising = lambda position: 0.5 + position / 160.0  # noqa: E731
+    assert pair.step([(0, p) for p in range(0, 200)], rng, key_scale=rising) == 0
+    assert pair.step([(0, p) for p in range(200, 420)], rng, key_scale=rising) == 0
+    assert pair.step([(0, p) for p in range(420, 452)], rng, key_scale=rising, fused=True) == 0
+    pair.check_contents(0)
 
 
 def test_table_operations_match_the_restatement(torch_gpu):
