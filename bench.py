@@ -178,11 +178,241 @@ def prefill_config(args, torch) -> dict:
     }
 
 
+def fill_slot(cache, torch, slot, first, count, chunk, layers, generator):
+    """Appends positions [first, first + count) of `slot` through step + append_rope in prompt chunks."""
+    buffer = torch.empty((chunk, cache.qkv_width), device="cuda")
+    for start in range(first, first + count, chunk):
+        size = min(chunk, first + count - start)
+        cache.step([(slot, p) for p in range(start, start + size)])
+        for layer in range(layers):
+            rows = buffer[:size]
+            rows.normal_(generator=generator)
+            cache.append_rope(layer, rows)
+    torch.cuda.synchronize()
+
+
+def apply_options(args, cache) -> None:
+    if args.split_keys:
+        cache.set_split_keys(args.split_keys)
+    if args.prefetch is not None:
+        from synapse_amd.native import OPTION_DECODE_PREFETCH
+
+        cache.set_option(OPTION_DECODE_PREFETCH, args.prefetch)
+
+
+def timed(torch, cache, run, repetitions, profile_every=1):
+    """Wall seconds per repetition of `run` (between synchronizations) and the cache's kernel profile."""
+    from synapse_amd.native import OPTION_PROFILE_EVERY
+
+    cache.set_option(OPTION_PROFILE_EVERY, profile_every)
+    cache.profile_begin()
+    torch.cuda.synchronize()
+    begin = time.perf_counter()
+    for index in range(repetitions):
+        run(index)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - begin
+    return elapsed / repetitions, cache.profile_end()
+
+
+def kernel_us(kernels, kind):
+    launches, ms = kernels.get(kind, (0, 0.0))
+    return ms * 1e3 / launches if launches else None
+
+
+def decode_line(args, *, metric, workload, tokens_per_step, seconds, bytes_per_step, layers, decode_bytes_per_launch,
+                kernels, data, extra=None):
+    decode_us = kernel_us(kernels, "decode")
+    decode_gbps = decode_bytes_per_launch / (decode_us * 1e-6) / 1e9 if decode_us else None
+    line = {
+        "metric": metric, "value": round(tokens_per_step / seconds, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(seconds * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16" if "FP16" in workload else "f32", "data": data,
+        "config": {"workload": workload, "layers": layers},
+        "hbm_gbps": round(bytes_per_step / seconds / 1e9, 1),
+        "hbm_frac_of_peak": round(bytes_per_step / seconds / 1e9 / PEAK_HBM_GBPS, 4),
+        "roofline": {"bound": "hbm", "kernel": "decode_kernel (fused append + split-K decode)",
+                     "achieved": round(decode_gbps, 1) if decode_gbps else None, "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(decode_gbps / PEAK_HBM_GBPS, 4) if decode_gbps else None,
+                     "traffic": None, "algorithmic_bytes_per_launch": int(decode_bytes_per_launch),
+                     "avg_launch_us": round(decode_us, 2) if decode_us else None,
+                     "kernels_ms": {kind: round(ms, 3) for kind, (count, ms) in kernels.items()}},
+    }
+    if extra:
+        line.update(extra)
+    return line
+
+
+def config_c1(args, torch) -> dict:
+    """Config C1: 0.5B shape (24 layers, 14 q / 2 KV heads, head_dim 64), FP32 KV, one sequence decoding over
+    4,096 cached tokens. One step = 24 x append_attention for the next position."""
+    from synapse_amd import PagedKvCache
+
+    layers, heads, kv_heads, d, cached = 24, 14, 2, 64, 4096
+    total = args.warmup + args.steps
+    cache = PagedKvCache(layers=layers, heads=heads, kv_heads=kv_heads, head_dim=d, max_positions=8192,
+                         growth_positions=1024, page_tokens=256, precision="f32", session_slots=1,
+                         step_tokens=512, max_pages=32)
+    cache.set_stream(torch.cuda.current_stream())
+    apply_options(args, cache)
+    cache.reserve(0, cached + total + 1)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(SEED + 1)
+    fill_slot(cache, torch, 0, 0, cached, 512, layers, generator)
+    qkv = torch.empty((layers, 1, cache.qkv_width), device="cuda").normal_(generator=generator)
+    out = torch.empty((layers, 1, heads * d), device="cuda")
+
+    def run(index):
+        cache.step([(0, cached + index)])
+        for layer in range(layers):
+            cache.append_attention(layer, qkv[layer], out[layer])
+
+    for index in range(args.warmup):
+        run(index)
+    seconds, kernels = timed(torch, cache, lambda i: run(args.warmup + i), args.steps, profile_every=layers // 2)
+    row = 2 * kv_heads * d * 4  # K + V bytes per position per layer (FP32)
+    keys = cached + args.warmup + (args.steps + 1) / 2
+    launch_bytes = keys * row + row + heads * d * 4 + 2 * kv_heads * d * 4
+    cache.close()
+    return decode_line(args, metric="C1 decode attn+KV-append tokens/s, 0.5B FP32 KV @4k ctx",
+                       workload="C1: Qwen2.5-0.5B-shaped single-sequence decode, FP32 KV, 4,096 cached tokens, "
+                                "24 layers", tokens_per_step=1, seconds=seconds,
+                       bytes_per_step=layers * (launch_bytes + heads * d * 4), layers=layers,
+                       decode_bytes_per_launch=launch_bytes, kernels=kernels,
+                       data=f"synthetic N(0,1) fp32 rows, torch seed {SEED + 1}")
+
+
+def config_c2(args, torch) -> dict:
+    """Config C2: 0.5B FP16 paged cache filled to 32,768 positions in 64 x 512-token appends, then single-sequence
+    decode steps over it, then a 1,024-position reserve that contracts the slot to 4 pages."""
+    from synapse_amd import PagedKvCache
+
+    layers, heads, kv_heads, d = 24, 14, 2, 64
+    filled = 32768
+    cache = PagedKvCache(layers=layers, heads=heads, kv_heads=kv_heads, head_dim=d, max_positions=65536,
+                         growth_positions=1024, page_tokens=256, precision="f16", session_slots=1,
+                         step_tokens=512, max_pages=256)
+    cache.set_stream(torch.cuda.current_stream())
+    apply_options(args, cache)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(SEED + 2)
+    rows = torch.empty((64, 512, cache.qkv_width), device="cuda").normal_(generator=generator)
+    torch.cuda.synchronize()
+
+    # Fill: 64 chunks x 24 layers of append_rope (RoPE + FP16 RNE store), growth through the capacity policy.
+    def fill_chunk(chunk):
+        cache.step([(0, p) for p in range(chunk * 512, chunk * 512 + 512)])
+        for layer in range(layers):
+            cache.append_rope(layer, rows[chunk])
+
+    fill_seconds, fill_kernels = timed(torch, cache, fill_chunk, 64)
+    width = cache.qkv_width * 4
+    fill_bytes = 512 * layers * (width + (heads + kv_heads) * d * 4 + 2 * kv_heads * d * 2)
+    qkv = torch.empty((layers, 1, cache.qkv_width), device="cuda").normal_(generator=generator)
+    out = torch.empty((layers, 1, heads * d), device="cuda")
+
+    def run(index):
+        cache.step([(0, filled + index)])
+        for layer in range(layers):
+            cache.append_attention(layer, qkv[layer], out[layer])
+
+    for index in range(args.warmup):
+        run(index)
+    seconds, kernels = timed(torch, cache, lambda i: run(args.warmup + i), args.steps, profile_every=layers // 2)
+    row = 2 * kv_heads * d * 2
+    keys = filled + args.warmup + (args.steps + 1) / 2
+    launch_bytes = keys * row + row + heads * d * 4 + 2 * kv_heads * d * 4
+    torch.cuda.synchronize()
+    begin = time.perf_counter()
+    cache.reserve(0, 1024)
+    cache.synchronize()
+    contract_ms = (time.perf_counter() - begin) * 1e3
+    info = cache.slot_info(0)
+    stats = cache.page_stats()
+    cache.close()
+    append_us = kernel_us(fill_kernels, "append")
+    return decode_line(
+        args, metric="C2 decode attn+KV-append tokens/s, 0.5B FP16 paged KV @32k ctx",
+        workload="C2: Qwen2.5-0.5B-shaped single sequence, FP16 paged KV (256-token pages): fill to 32,768 in "
+                 "64 x 512-token appends, decode, contract to 1,024", tokens_per_step=1, seconds=seconds,
+        bytes_per_step=layers * (launch_bytes + heads * d * 4), layers=layers, decode_bytes_per_launch=launch_bytes,
+        kernels=kernels, data=f"synthetic N(0,1) fp32 rows, torch seed {SEED + 2}",
+        extra={"fill": {"ms": round(fill_seconds * 64 * 1e3, 3), "tokens_per_s": round(512 / fill_seconds, 1),
+                        "append_avg_launch_us": round(append_us, 2) if append_us else None,
+                        "append_gbps": round(fill_bytes / layers / (append_us * 1e-6) / 1e9, 1) if append_us else None,
+                        "kernels_ms": {kind: round(ms, 3) for kind, (count, ms) in fill_kernels.items()}},
+               "contract": {"ms": round(contract_ms, 3), "slot": info, "used_pages": stats["used_pages"],
+                            "free_pages": stats["free_pages"]}})
+
+
+def config_c4(args, torch) -> dict:
+    """Config C4: a 30,000-token FP16 prefix forked copy-on-write into 8 sequences; each appends a distinct 64-token
+    suffix (one step, prompt path, copying the shared partial page), then decodes. Unique bytes count the shared
+    prefix once per layer."""
+    from synapse_amd import PagedKvCache
+
+    layers, heads, kv_heads, d = LAYERS, HEADS, KV_HEADS, HEAD_DIM
+    prefix, forks = 30000, 8
+    cache = PagedKvCache(layers=layers, heads=heads, kv_heads=kv_heads, head_dim=d, max_positions=32768,
+                         growth_positions=1024, page_tokens=256, precision="f16", session_slots=forks + 1,
+                         step_tokens=4096, max_pages=160)
+    cache.set_stream(torch.cuda.current_stream())
+    apply_options(args, cache)
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(SEED + 4)
+    cache.reserve(0, prefix)
+    fill_slot(cache, torch, 0, 0, prefix, 4096, layers, generator)
+    for target in range(1, forks + 1):
+        cache.fork(0, target)
+    suffix = torch.empty((64 * forks, cache.qkv_width), device="cuda").normal_(generator=generator)
+    suffix_out = torch.empty((64 * forks, heads * d), device="cuda")
+
+    def suffix_step(_):
+        cache.step([(slot, prefix + j) for slot in range(1, forks + 1) for j in range(64)])
+        for layer in range(layers):
+            cache.append_attention(layer, suffix, suffix_out)
+
+    suffix_seconds, suffix_kernels = timed(torch, cache, suffix_step, 1)
+    qkv = torch.empty((layers, forks, cache.qkv_width), device="cuda").normal_(generator=generator)
+    out = torch.empty((layers, forks, heads * d), device="cuda")
+
+    def run(index):
+        cache.step([(slot, prefix + 64 + index) for slot in range(1, forks + 1)])
+        for layer in range(layers):
+            cache.append_attention(layer, qkv[layer], out[layer])
+
+    for index in range(args.warmup):
+        run(index)
+    seconds, kernels = timed(torch, cache, lambda i: run(args.warmup + i), args.steps, profile_every=layers // 2)
+    row = 2 * kv_heads * d * 2
+    own = 64 + args.warmup + (args.steps + 1) / 2  # each fork's own positions (suffix + decoded), average
+    unique = prefix * row + forks * own * row
+    logical = forks * (prefix + own) * row
+    q_rows = forks * (heads * d * 4 + 2 * kv_heads * d * 4)
+    launch_unique = unique + forks * row + q_rows
+    launch_logical = logical + forks * row + q_rows
+    cache.close()
+    line = decode_line(
+        args, metric="C4 decode attn+KV-append tokens/s, 7B FP16, 8 COW forks of a 30,000-token prefix",
+        workload="C4: Qwen2.5-7B-shaped prefix reuse: 30,000-token FP16 prefix forked copy-on-write into 8 "
+                 "sequences, 64-token suffix each, then batched decode, 28 layers", tokens_per_step=forks,
+        seconds=seconds, bytes_per_step=layers * (launch_unique + forks * heads * d * 4), layers=layers,
+        decode_bytes_per_launch=launch_unique, kernels=kernels, data=f"synthetic N(0,1) fp32 rows, torch seed {SEED + 4}",
+        extra={"suffix_step_ms": round(suffix_seconds * 1e3, 3),
+               "suffix_kernels_ms": {kind: round(ms, 3) for kind, (count, ms) in suffix_kernels.items()}})
+    decode_us = kernel_us(kernels, "decode")
+    if decode_us:
+        line["roofline"]["logical_gbps"] = round(launch_logical / (decode_us * 1e-6) / 1e9, 1)
+        line["roofline"]["logical_bytes_per_launch"] = int(launch_logical)
+    return line
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--config", choices=["c3", "c5"], default="c3",
-                        help="c3: the BASELINE metric (default); c5: chunked-prefill MFMA throughput")
+    parser.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5"], default="c3",
+                        help="c3: the BASELINE metric (default); c1, c2, c4: the other decode configurations; "
+                             "c5: chunked-prefill MFMA throughput")
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--split-keys", type=int, default=None)
@@ -206,8 +436,9 @@ def main() -> None:
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a HIP device")
     torch.cuda.set_device(0)
-    if args.config == "c5":
-        print(json.dumps(prefill_config(args, torch)), flush=True)
+    if args.config != "c3":
+        runner = {"c1": config_c1, "c2": config_c2, "c4": config_c4, "c5": prefill_config}[args.config]
+        print(json.dumps(runner(args, torch)), flush=True)
         return
     lengths = lengths_for(SEED + CONFIG_OFFSET)
     total_steps = args.warmup + args.steps

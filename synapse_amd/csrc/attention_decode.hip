@@ -328,16 +328,35 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
         const floatx4* values =
             reinterpret_cast<const floatx4*>(page + value_region + static_cast<size_t>(within) * D) + lane;
 
+        // The step's K and V fragments are requested together: one memory round trip per step.
+        floatx4 key_fragment[4][D / 16];
+        floatx4 value_fragment[4][D / 16];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) {
+                key_fragment[t][c] = load_fragment(keys + (t * (D / 16) + c) * 64);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int mt = 0; mt < D / 16; ++mt) {
+                value_fragment[t][mt] = load_fragment(values + (t * (D / 16) + mt) * 64);
+            }
+        }
+        // Keeps the scheduler from sinking the loads towards their uses (which would serialize the round trips).
+        __builtin_amdgcn_sched_barrier(0);
         floatx4 scores[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             scores[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int c = 0; c < D / 16; ++c) {
-                const floatx4 k = load_fragment(keys + (t * (D / 16) + c) * 64);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    scores[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(k[i], query[c][i], scores[t], 0, 0, 0);
+                    scores[t] =
+                        __builtin_amdgcn_mfma_f32_16x16x4f32(key_fragment[t][c][i], query[c][i], scores[t], 0, 0, 0);
                 }
             }
         }
@@ -359,10 +378,10 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
             for (int mt = 0; mt < D / 16; ++mt) {
-                const floatx4 v = load_fragment(values + (t * (D / 16) + mt) * 64);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    state.out[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[i], scores[t][i], state.out[mt], 0, 0, 0);
+                    state.out[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(value_fragment[t][mt][i], scores[t][i],
+                                                                         state.out[mt], 0, 0, 0);
                 }
             }
         }
@@ -466,7 +485,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
 // Split merge (attention_reduce.metal:5-40): one wave per (merge entry, query head of the group, 64 dims). The
 // lanes first load the (max, sum) of 64 splits at once, reduce the max over splits with a positive sum and turn
 // each split into its weight exp2(m - max); the output is then the weighted sum of the splits' rows over the
-// weighted sums, every row load independent of the others.
+// weighted sums, every row load independent of the others. Rows with more than 64 splits are merged in two
+// launches: blocks of 64 splits into intermediate partial rows (output_row >= 0), then those.
 template <int D>
 __global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int first, int count) {
     const int group = a.geo.group;
@@ -483,6 +503,7 @@ __global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int
     const size_t stride = static_cast<size_t>(group) * D;
     float sum = 0.0f;
     float value = 0.0f;
+    float maximum = kNegativeInfinity;
     if (merge.count <= 64) {
         // One round of loads: every split's row value and (max, sum) are requested before any is used.
         const float* rows = a.partial_out + (static_cast<size_t>(merge.first_row) * group + head) * D + 64 * chunk + lane;
@@ -498,7 +519,7 @@ __global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int
             split_max = ml[row * 2];
             split_sum = ml[row * 2 + 1];
         }
-        float maximum = split_sum > 0.0f ? split_max : kNegativeInfinity;
+        maximum = split_sum > 0.0f ? split_max : kNegativeInfinity;
 #pragma unroll
         for (int offset = 32; offset > 0; offset >>= 1) {
             maximum = fmaxf(maximum, __shfl_xor(maximum, offset));
@@ -511,7 +532,6 @@ __global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int
             value += values[split] * w;
         }
     } else {
-        float maximum = kNegativeInfinity;
         for (int base = 0; base < merge.count; base += 64) {
             const int split = base + lane;
             if (split < merge.count) {
@@ -545,6 +565,17 @@ __global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
         sum += __shfl_xor(sum, offset);
+    }
+    if (merge.output_row >= 0) {
+        // First level of a two-level merge: the combination is itself a partial row (unnormalized values
+        // relative to `maximum`, with their weighted sum).
+        const size_t row = static_cast<size_t>(merge.output_row) * group + head;
+        a.partial_out[row * D + 64 * chunk + lane] = value;
+        if (chunk == 0 && lane == 0) {
+            a.partial_ml[row * 2] = maximum;
+            a.partial_ml[row * 2 + 1] = sum;
+        }
+        return;
     }
     a.output[static_cast<size_t>(merge.token) * a.out_stride +
              static_cast<size_t>(merge.kv_head * group + head) * D + 64 * chunk + lane] = value / sum;

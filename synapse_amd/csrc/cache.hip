@@ -223,8 +223,8 @@ struct SynapseKvCache {
     bool step_ready = false;
     int32_t step_count = 0;
     int32_t decode_workers = 0;
-    int32_t decode_merges = 0;
-    int32_t prefill_merges = 0;
+    int32_t first_level_merges = 0;  // merges[0, first_level_merges) run before the rest
+    int32_t merges = 0;
     int32_t prefill_items = 0;
     int32_t decode_waves = 1024;  // resident decode waves on the device
     bool fusable = false;         // the step can append and attend in one decode launch
@@ -524,7 +524,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             const int32_t pieces = static_cast<int32_t>(segments.size() - first_segment);
             if (pieces > 1) {
                 const int32_t merge = static_cast<int32_t>(merges.size());
-                merges.push_back(MergeItem{row.token, row.kv_head, partial_rows, pieces});
+                merges.push_back(MergeItem{row.token, row.kv_head, partial_rows, pieces, -1, {0, 0, 0}});
                 for (int32_t piece = 0; piece < pieces; ++piece) {
                     segments[first_segment + piece].row = partial_rows + piece;
                     segments[first_segment + piece].merge = merge;
@@ -556,7 +556,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
                         prefill_merges.push_back(MergeItem{first + j, static_cast<int32_t>(kv_head),
                                                            partial_rows + j * stride +
                                                                static_cast<int32_t>(kv_head) * splits,
-                                                           splits});
+                                                           splits, -1, {0, 0, 0}});
                     }
                 }
             }
@@ -575,8 +575,28 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             }
         }
     }
-    const int32_t decode_merges = static_cast<int32_t>(merges.size());
     merges.insert(merges.end(), prefill_merges.begin(), prefill_merges.end());
+    // Merges over more than 64 partial rows first combine blocks of 64 rows into intermediate partial rows (one
+    // launch), then merge those (a second launch); the merge kernel's single load round covers 64 rows.
+    std::vector<MergeItem> first_level;
+    std::vector<MergeItem> final_level;
+    for (MergeItem merge : merges) {
+        if (merge.count <= 64) {
+            final_level.push_back(merge);
+            continue;
+        }
+        const int32_t blocks = (merge.count + 63) / 64;
+        for (int32_t block = 0; block < blocks; ++block) {
+            first_level.push_back(MergeItem{merge.token, merge.kv_head, merge.first_row + 64 * block,
+                                            std::min<int32_t>(64, merge.count - 64 * block), partial_rows + block,
+                                            {0, 0, 0}});
+        }
+        final_level.push_back(MergeItem{merge.token, merge.kv_head, partial_rows, blocks, -1, {0, 0, 0}});
+        partial_rows += blocks;
+    }
+    const int32_t first_level_merges = static_cast<int32_t>(first_level.size());
+    merges = std::move(first_level);
+    merges.insert(merges.end(), final_level.begin(), final_level.end());
 
     const size_t tokens_bytes = static_cast<size_t>(count) * sizeof(SynapseKvBatchToken);
     cache.tokens_offset = 0;
@@ -598,8 +618,8 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.uploader.copy(cache.blob.pointer, total, cache.stream);
     cache.step_count = count;
     cache.decode_workers = workers;
-    cache.decode_merges = decode_merges;
-    cache.prefill_merges = static_cast<int32_t>(prefill_merges.size());
+    cache.first_level_merges = first_level_merges;
+    cache.merges = static_cast<int32_t>(merges.size());
     cache.prefill_items = static_cast<int32_t>(prefill.size());
     // The fused append + decode launch needs every token to own its slot: no token may read another token's
     // position of the same step, and each (token, KV head) row appends its own position only.
@@ -861,8 +881,13 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
               "prefill attention");
     check_hip(launch_decode(launch_for(cache, SYNAPSE_KV_KERNEL_DECODE, args.workers > 0), args, fp16, cache.prefetch != 0),
               "decode attention");
-    const int merges = cache.decode_merges + cache.prefill_merges;
-    check_hip(launch_merge(launch_for(cache, SYNAPSE_KV_KERNEL_MERGE, merges > 0), args, 0, merges), "split merge");
+    const int first_level = cache.first_level_merges;
+    if (first_level > 0) {
+        check_hip(launch_merge(launch_for(cache, SYNAPSE_KV_KERNEL_MERGE, true), args, 0, first_level), "split merge");
+    }
+    const int final_level = cache.merges - first_level;
+    check_hip(launch_merge(launch_for(cache, SYNAPSE_KV_KERNEL_MERGE, final_level > 0), args, first_level, final_level),
+              "split merge");
 }
 
 }  // namespace

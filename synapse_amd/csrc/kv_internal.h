@@ -72,6 +72,8 @@ struct MergeItem {
     int32_t kv_head;
     int32_t first_row;
     int32_t count;
+    int32_t output_row;  // -1: normalize into the output; else write the combination as this partial row
+    int32_t pad[3];
 };
 
 // A prefill work item: `count` (<= kPrefillTokens) consecutive tokens of one prompt run (consecutive positions of
