@@ -451,12 +451,7 @@ def main() -> None:
                          precision="f16", session_slots=SEQUENCES, step_tokens=4096, max_pages=pages)
     stream = torch.cuda.current_stream()
     cache.set_stream(stream)
-    if args.split_keys:
-        cache.set_split_keys(args.split_keys)
-    if args.prefetch is not None:
-        from synapse_amd.native import OPTION_DECODE_PREFETCH
-
-        cache.set_option(OPTION_DECODE_PREFETCH, args.prefetch)
+    apply_options(args, cache)
     for slot, length in enumerate(lengths.tolist()):
         cache.reserve(slot, length + total_steps + 1)
     generator = torch.Generator(device="cuda")

@@ -424,7 +424,7 @@ __device__ void finish_segment(const AttentionArgs& a, const DecodeSegment& seg,
 
 // Fused append (synapse_rope_kv, elementwise.metal:73-126) of one (token, KV head) by the wave that owns the row's
 // last segment, i.e. the only wave that reads the token's own position: rotate K, store K and V in the page's
-// element type, then make the stores visible to this wave's loads. The qkv rows are read, not rewritten.
+// element type, then wait for the stores before this wave's loads. The qkv rows are read, not rewritten.
 template <typename T, int D>
 __device__ void append_row(const AttentionArgs& a, const DecodeSegment& seg) {
     const Geometry& geo = a.geo;
@@ -451,7 +451,9 @@ __device__ void append_row(const AttentionArgs& a, const DecodeSegment& seg) {
     for (int dim = lane; dim < D; dim += 64) {
         values[value_offset<T>(D, within, dim)] = static_cast<T>(value[dim]);
     }
-    __threadfence();
+    // The stores reach this XCD's L2 before the wave's own loads of the block are issued; no other wave reads the
+    // row's region in this launch, so no device-wide fence (L2 write-back) is needed.
+    __builtin_amdgcn_s_waitcnt(0);
 }
 
 template <int D, bool F16, bool PREFETCH>

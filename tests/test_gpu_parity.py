@@ -190,6 +190,24 @@ def test_append_attention_matches_the_restatement(torch_gpu, heads, kv_heads, he
         pair.check_contents(slot)
 
 
+def test_rows_cut_into_many_pieces(torch_gpu):
+    """Rows of 79 and 2 64-key steps with one step per worker: the long rows' 79 partials go through the two-level
+    merge (blocks of 64 partial rows, then the blocks); three layers reuse one plan."""
+    say("many pieces")
+    pair = Pair(torch_gpu, heads=28, kv_heads=4, head_dim=128, max_positions=8192, growth=1024, max_pages=40,
+                layers=3, slots=2)
+    rng = np.random.default_rng(77)
+    for first in range(0, 5000, 256):
+        assert pair.step([(0, p) for p in range(first, min(5000, first + 256))], rng, attend=False) == 0
+    assert pair.step([(1, p) for p in range(100)], rng, attend=False) == 0
+    lengths = [5000, 100]
+    for split, fused in ((64, True), (64, False), (128, True), (256, False)):
+        pair.gpu.set_split_keys(split)
+        assert pair.step([(slot, lengths[slot]) for slot in range(2)], rng, fused=fused) == 0
+        lengths = [length + 1 for length in lengths]
+    pair.check_contents(0)
+
+
 def test_single_position_and_page_boundaries(torch_gpu):
     say("page boundaries")
     pair = Pair(torch_gpu, page=64, growth=64, max_pages=64, heads=28, kv_heads=4, head_dim=128)
