@@ -40,11 +40,12 @@ extern "C" {
 #define SYNAPSE_KV_F16 1u
 
 /* Tuning options for synapse_kv_set_option. */
-#define SYNAPSE_KV_OPTION_SPLIT_KEYS 1u     /* fewest keys per decode wave worker; a multiple of 64 (default 256) */
+#define SYNAPSE_KV_OPTION_SPLIT_KEYS 1u     /* fewest keys per decode wave worker; a multiple of 64 (default 64) */
 #define SYNAPSE_KV_OPTION_PREFILL_RUNS 2u   /* 1: FP16 prompt runs use the MFMA prefill kernel (default); 0: decode path */
 #define SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS 3u /* keys per prefill split-K work item, a multiple of 64; 0 (default): fill the device */
 #define SYNAPSE_KV_OPTION_DECODE_PREFETCH 4u /* 1: FP16 decode keeps the next step's loads in flight (two register sets) */
 #define SYNAPSE_KV_OPTION_PROFILE_EVERY 5u   /* profile mode times every n-th launch of each kernel kind (default 1) */
+#define SYNAPSE_KV_OPTION_SHARED_PREFIX 6u  /* 1 (default): FP16 decode reads pages shared by several step tokens once */
 
 /* GpuDeviceInfo (native/synapse-gpu/src/Features/GpuKernels/mod.rs:20-31), 152 bytes. */
 typedef struct SynapseKvDeviceInfo {
@@ -104,7 +105,7 @@ typedef struct SynapseKvPageStats {
 #define SYNAPSE_KV_KERNEL_APPEND 2  /* RoPE + KV append */
 #define SYNAPSE_KV_KERNEL_DECODE 3  /* split-K decode attention (with the fused append when used) */
 #define SYNAPSE_KV_KERNEL_MERGE 4   /* split merge */
-#define SYNAPSE_KV_KERNEL_PREFILL 5 /* prompt-run attention */
+#define SYNAPSE_KV_KERNEL_PREFILL 5 /* prompt-run attention, and shared-prefix pages read once for their sharers */
 #define SYNAPSE_KV_KERNEL_GATHER 6  /* KV read-back */
 typedef struct SynapseKvProfile {
     uint64_t launches[8];

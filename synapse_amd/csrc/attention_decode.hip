@@ -114,160 +114,174 @@ struct Fragments16 {
     half8 value[2][D / 16];
 };
 
-// One token's keys [key_begin, key_end) for one KV head, FP16 pages. With PREFETCH the next step's fragments are
-// loaded before the current step is computed.
-template <int D, bool PREFETCH>
-__device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
-    const Geometry& geo = a.geo;
-    const int lane = threadIdx.x & 63;
-    const int r = lane & 15;
-    const int g = lane >> 4;
-    // B operand of S^T = K Q^T: lane (g, r) holds dims 32*ks + 8*g .. +7 of query head r of the group. With
-    // D/2 = 32 * (D/64) the RoPE partner of dim i < D/2 (i + D/2) sits in the same lane at ks + D/64.
-    half8 query[D / 32];
-    {
-        const bool valid = r < geo.group;
-        const float* q = a.qkv + static_cast<size_t>(seg.token) * a.qkv_stride +
-                         static_cast<size_t>(seg.kv_head * geo.group + (valid ? r : 0)) * D;
-        float values[D / 32][8];
+// B operand of S^T = K Q^T for one lane (g, r): dims 32*ks + 8*g .. +7 of query head `head` of `token`, rotated
+// (when the call asks for RoPE) at the token's position, in FP16; zero when the column is unused. With
+// D/2 = 32 * (D/64) the RoPE partner of dim i < D/2 (i + D/2) sits in the same lane at ks + D/64.
+template <int D>
+__device__ inline void load_query_f16(const AttentionArgs& a, int token, int head, bool valid, half8 (&query)[D / 32]) {
+    const int g = (threadIdx.x & 63) >> 4;
+    const float* q = a.qkv + static_cast<size_t>(token) * a.qkv_stride + static_cast<size_t>(head) * D;
+    float values[D / 32][8];
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) {
-            const floatx4 lo = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g);
-            const floatx4 hi = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g + 4);
+    for (int ks = 0; ks < D / 32; ++ks) {
+        const floatx4 lo = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g);
+        const floatx4 hi = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g + 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                values[ks][j] = lo[j];
-                values[ks][j + 4] = hi[j];
-            }
+        for (int j = 0; j < 4; ++j) {
+            values[ks][j] = lo[j];
+            values[ks][j + 4] = hi[j];
         }
-        if (a.rotate) {
-            const int position = a.tokens[seg.token].position;
-            const float* cosines = a.cosines + static_cast<size_t>(position) * (D / 2);
-            const float* sines = a.sines + static_cast<size_t>(position) * (D / 2);
+    }
+    if (a.rotate) {
+        const int position = a.tokens[token].position;
+        const float* cosines = a.cosines + static_cast<size_t>(position) * (D / 2);
+        const float* sines = a.sines + static_cast<size_t>(position) * (D / 2);
 #pragma unroll
-            for (int ks = 0; ks < D / 64; ++ks) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int i = 32 * ks + 8 * g + j;
-                    rotate_pair(values[ks][j], values[ks + D / 64][j], cosines[i], sines[i], values[ks][j],
-                                values[ks + D / 64][j]);
-                }
-            }
-        }
-#pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) {
+        for (int ks = 0; ks < D / 64; ++ks) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                query[ks][j] = valid ? static_cast<_Float16>(values[ks][j]) : static_cast<_Float16>(0.0f);
+                const int i = 32 * ks + 8 * g + j;
+                rotate_pair(values[ks][j], values[ks + D / 64][j], cosines[i], sines[i], values[ks][j],
+                            values[ks + D / 64][j]);
             }
         }
     }
-    const int slot = a.tokens[seg.token].slot;
-    const int32_t* table = geo.block_table + static_cast<size_t>(slot) * geo.pages_per_slot;
-    const size_t key_region = region_offset(geo, 0, seg.kv_head);
-    const size_t value_region = region_offset(geo, 1, seg.kv_head);
-    const int page_tokens = geo.page_tokens;
-    // The A operand of QK^T tile t = 2h + u holds key 32h + 8*(r/4) + 4u + r%4 in row r (the page layout stores it
-    // there), so the C tile puts key 32h + 8g + 4u + i on this lane group's element 4u + i of the PV B operand.
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            query[ks][j] = valid ? static_cast<_Float16>(values[ks][j]) : static_cast<_Float16>(0.0f);
+        }
+    }
+}
 
-    auto fetch = [&](int key0, Fragments16<D>& fragments) {
-        const int logical = key0 / page_tokens;
-        const int within = key0 - logical * page_tokens;
-        const _Float16* page = reinterpret_cast<const _Float16*>(
-            geo.pool + static_cast<uint64_t>(table[logical]) * geo.page_bytes);
-        // 64-key blocks in fragment order: every load below is one contiguous 1 KiB wave load.
-        const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D) + lane;
-        const half8* values =
-            reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D) + lane;
+// Loads the FP16 fragments of the 64-key block holding key0 (a multiple of 64) of one (slot table, KV head).
+template <int D>
+__device__ inline void fetch_f16(const Geometry& geo, const int32_t* table, size_t key_region, size_t value_region,
+                                 int key0, Fragments16<D>& fragments) {
+    const int lane = threadIdx.x & 63;
+    const int logical = key0 / geo.page_tokens;
+    const int within = key0 - logical * geo.page_tokens;
+    const _Float16* page =
+        reinterpret_cast<const _Float16*>(geo.pool + static_cast<uint64_t>(table[logical]) * geo.page_bytes);
+    // 64-key blocks in fragment order: every load below is one contiguous 1 KiB wave load.
+    const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D) + lane;
+    const half8* values = reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D) + lane;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 4; ++t) {
 #pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) {
-                fragments.key[t][ks] = load_fragment(keys + (t * (D / 32) + ks) * 64);
-            }
+        for (int ks = 0; ks < D / 32; ++ks) {
+            fragments.key[t][ks] = load_fragment(keys + (t * (D / 32) + ks) * 64);
         }
+    }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int mt = 0; mt < D / 16; ++mt) {
-                fragments.value[h][mt] = load_fragment(values + (h * (D / 16) + mt) * 64);
-            }
-        }
-    };
-    auto consume = [&](int key0, const Fragments16<D>& fragments) {
-        floatx4 scores[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            scores[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) {
-                scores[t] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(fragments.key[t][ks], query[ks], scores[t], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = key0 + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
-                scores[t][i] = key < seg.key_end ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
-            }
-        }
-        const float alpha = softmax_step(scores, state.maximum, state.sum);
-        half8 probability[2];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                probability[t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(scores[t][i]);
-            }
-        }
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
         for (int mt = 0; mt < D / 16; ++mt) {
-            state.out[mt] *= alpha;
+            fragments.value[h][mt] = load_fragment(values + (h * (D / 16) + mt) * 64);
         }
+    }
+}
+
+// One 64-key step for one column tile: S^T = K Q^T, masked scale to log2 units, online softmax, O^T += V^T P^T.
+// The A operand of QK^T tile t = 2h + u holds key 32h + 8*(r/4) + 4u + r%4 in row r (the page layout stores it
+// there), so the C tile puts key 32h + 8g + 4u + i on this lane group's element 4u + i of the PV B operand.
+template <int D>
+__device__ inline void step_f16(const Fragments16<D>& fragments, const half8 (&query)[D / 32], WaveState<D>& state,
+                                int key0, int key_end, float scale_log2) {
+    const int g = (threadIdx.x & 63) >> 4;
+    floatx4 scores[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+    for (int t = 0; t < 4; ++t) {
+        scores[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int mt = 0; mt < D / 16; ++mt) {
-                state.out[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fragments.value[h][mt], probability[h],
-                                                                       state.out[mt], 0, 0, 0);
-            }
+        for (int ks = 0; ks < D / 32; ++ks) {
+            scores[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fragments.key[t][ks], query[ks], scores[t], 0, 0, 0);
         }
-    };
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = key0 + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
+            scores[t][i] = key < key_end ? scores[t][i] * scale_log2 : kNegativeInfinity;
+        }
+    }
+    const float alpha = softmax_step(scores, state.maximum, state.sum);
+    half8 probability[2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            probability[t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(scores[t][i]);
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < D / 16; ++mt) {
+        state.out[mt] *= alpha;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int mt = 0; mt < D / 16; ++mt) {
+            state.out[mt] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(fragments.value[h][mt], probability[h], state.out[mt], 0, 0, 0);
+        }
+    }
+}
+
+// Keys [key_begin, key_end) of one KV head through the block table `table` against one column tile of queries,
+// FP16 pages. With PREFETCH the next step's fragments are loaded before the current step is computed.
+template <int D, bool PREFETCH>
+__device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, int kv_head, int key_begin,
+                                  int key_end, const half8 (&query)[D / 32], WaveState<D>& state) {
+    const Geometry& geo = a.geo;
+    const size_t key_region = region_offset(geo, 0, kv_head);
+    const size_t value_region = region_offset(geo, 1, kv_head);
     if constexpr (!PREFETCH) {
-        for (int key0 = seg.key_begin; key0 < seg.key_end; key0 += kStepKeys) {
+        for (int key0 = key_begin; key0 < key_end; key0 += kStepKeys) {
             Fragments16<D> fragments;
-            fetch(key0, fragments);
-            consume(key0, fragments);
+            fetch_f16<D>(geo, table, key_region, value_region, key0, fragments);
+            step_f16<D>(fragments, query, state, key0, key_end, a.scale_log2);
         }
     } else {
         // Two register sets: the loads of the next step are in flight while the current step computes.
         Fragments16<D> even;
         Fragments16<D> odd;
-        int key0 = seg.key_begin;
-        fetch(key0, even);
+        int key0 = key_begin;
+        fetch_f16<D>(geo, table, key_region, value_region, key0, even);
         while (true) {
-            const bool more = key0 + kStepKeys < seg.key_end;
+            const bool more = key0 + kStepKeys < key_end;
             if (more) {
-                fetch(key0 + kStepKeys, odd);
+                fetch_f16<D>(geo, table, key_region, value_region, key0 + kStepKeys, odd);
             }
-            consume(key0, even);
+            step_f16<D>(even, query, state, key0, key_end, a.scale_log2);
             if (!more) {
                 break;
             }
             key0 += kStepKeys;
-            const bool after = key0 + kStepKeys < seg.key_end;
+            const bool after = key0 + kStepKeys < key_end;
             if (after) {
-                fetch(key0 + kStepKeys, even);
+                fetch_f16<D>(geo, table, key_region, value_region, key0 + kStepKeys, even);
             }
-            consume(key0, odd);
+            step_f16<D>(odd, query, state, key0, key_end, a.scale_log2);
             if (!after) {
                 break;
             }
             key0 += kStepKeys;
         }
     }
+}
+
+// One token's keys [key_begin, key_end) for one KV head, FP16 pages.
+template <int D, bool PREFETCH>
+__device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
+    const Geometry& geo = a.geo;
+    const int r = threadIdx.x & 15;
+    half8 query[D / 32];
+    load_query_f16<D>(a, seg.token, seg.kv_head * geo.group + (r < geo.group ? r : 0), r < geo.group, query);
+    const int32_t* table = geo.block_table + static_cast<size_t>(a.tokens[seg.token].slot) * geo.pages_per_slot;
+    attend_blocks_f16<D, PREFETCH>(a, table, seg.kv_head, seg.key_begin, seg.key_end, query, state);
 }
 
 // One token's keys [key_begin, key_end) for one KV head, FP32 pages.

@@ -12,6 +12,10 @@
 // kernel's 64-key step:
 // S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16, every K/V fragment loaded once and used by all
 // column tiles. Causal masking is a per-element compare against the column's position.
+//
+// The same kernel reads copy-on-write prefixes once for several sequences: a listed item's columns are the decode
+// tokens of forks that share the item's pages (unmasked, each rotated at its own position), so every shared K/V
+// block goes through HBM once per item instead of once per fork.
 
 #include <type_traits>
 
@@ -76,17 +80,20 @@ __device__ inline void barrier_after_copies() {
     asm volatile("" ::: "memory");
 }
 
-template <int D, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a) {
-    constexpr int NT = kPrefillTiles;
-    const PrefillItem item = a.prefill[blockIdx.x];
+// NT column tiles of 16 tokens per wave: kPrefillTiles for prompt runs, 1 for listed items of at most 16 members.
+template <int D, int WAVES, int NT>
+__global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a, int first_item) {
+    const PrefillItem item = a.prefill[first_item + blockIdx.x];
     const Geometry& geo = a.geo;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // query head within the group
     const int lane = threadIdx.x & 63;
     const int r = lane & 15;
     const int g = lane >> 4;
     const int head = item.kv_head * geo.group + wave;
-    const SynapseKvBatchToken first = a.tokens[item.first_token];
+    const bool listed = item.listed != 0;
+    // Step token of column j: the run's j-th token, or the j-th listed member.
+    auto column_token = [&](int j) { return listed ? a.members[item.first_token + j] : item.first_token + j; };
+    const SynapseKvBatchToken first = a.tokens[column_token(0)];
     const int first_position = first.position;
 
     // B operands of S^T = K Q^T: tile c, lane (g, r) holds dims 32*ks + 8*g .. +7 of token 16*c + r; the RoPE
@@ -96,7 +103,7 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
     for (int c = 0; c < NT; ++c) {
         const int j = 16 * c + r;
         const bool valid = j < item.count;
-        const int token = item.first_token + (valid ? j : 0);
+        const int token = column_token(valid ? j : 0);
         const float* q = a.qkv + static_cast<size_t>(token) * a.qkv_stride + static_cast<size_t>(head) * D;
         float values[D / 32][8];
 #pragma unroll
@@ -110,7 +117,7 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
             }
         }
         if (a.rotate) {
-            const int position = first_position + (valid ? j : 0);
+            const int position = listed ? a.tokens[token].position : first_position + (valid ? j : 0);
             const float* cosines = a.cosines + static_cast<size_t>(position) * (D / 2);
             const float* sines = a.sines + static_cast<size_t>(position) * (D / 2);
 #pragma unroll
@@ -156,9 +163,9 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
     const size_t value_region = ((static_cast<size_t>(geo.layer) * 2 + 1) * geo.kv_heads + item.kv_head) * region;
     const int page_tokens = geo.page_tokens;
     // Keys past the block's last token are masked for every column; steps ending at or before the block's first
-    // token (and inside the split) are visible to every column.
-    const int key_stop = min(item.key_end, first_position + item.count);
-    const int unmasked_stop = min(item.key_end, first_position + 1);
+    // token (and inside the split) are visible to every column. A listed item's keys are visible to every column.
+    const int key_stop = listed ? item.key_end : min(item.key_end, first_position + item.count);
+    const int unmasked_stop = listed ? item.key_end : min(item.key_end, first_position + 1);
     const int steps = key_stop > item.key_begin ? (key_stop - item.key_begin + kStepKeys - 1) / kStepKeys : 0;
     const int clean = unmasked_stop > item.key_begin ? min(steps, (unmasked_stop - item.key_begin) / kStepKeys) : 0;
 
@@ -428,7 +435,7 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
         if (j >= item.count) {
             continue;
         }
-        const int token = item.first_token + j;
+        const int token = column_token(j);
         if (item.row < 0) {
             float* destination = a.output + static_cast<size_t>(token) * a.out_stride + static_cast<size_t>(head) * D;
             const float inverse = 1.0f / sum;
@@ -451,14 +458,32 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
     }
 }
 
-template <int WAVES>
-hipError_t launch_prefill_for(const Launch& launch, const AttentionArgs& args, dim3 grid, dim3 block) {
+template <int WAVES, int NT>
+hipError_t launch_prefill_for(const Launch& launch, const AttentionArgs& args, int first, dim3 grid, dim3 block) {
     if (args.geo.head_dim == 128) {
-        SYNAPSE_KV_LAUNCH((prefill_f16_kernel<128, WAVES>), grid, block, launch, args);
+        SYNAPSE_KV_LAUNCH((prefill_f16_kernel<128, WAVES, NT>), grid, block, launch, args, first);
     } else {
-        SYNAPSE_KV_LAUNCH((prefill_f16_kernel<64, WAVES>), grid, block, launch, args);
+        SYNAPSE_KV_LAUNCH((prefill_f16_kernel<64, WAVES, NT>), grid, block, launch, args, first);
     }
     return hipGetLastError();
+}
+
+template <int NT>
+hipError_t launch_prefill_tiles(const Launch& launch, const AttentionArgs& args, int first, int items) {
+    const dim3 grid(items);
+    const dim3 block(args.geo.group * 64);
+    // One wave per query head of the group (validated at cache creation: 1..8).
+    switch (args.geo.group) {
+        case 1: return launch_prefill_for<1, NT>(launch, args, first, grid, block);
+        case 2: return launch_prefill_for<2, NT>(launch, args, first, grid, block);
+        case 3: return launch_prefill_for<3, NT>(launch, args, first, grid, block);
+        case 4: return launch_prefill_for<4, NT>(launch, args, first, grid, block);
+        case 5: return launch_prefill_for<5, NT>(launch, args, first, grid, block);
+        case 6: return launch_prefill_for<6, NT>(launch, args, first, grid, block);
+        case 7: return launch_prefill_for<7, NT>(launch, args, first, grid, block);
+        case 8: return launch_prefill_for<8, NT>(launch, args, first, grid, block);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <int D>
@@ -466,14 +491,14 @@ int prefill_blocks_per_cu(int group) {
     int blocks = 0;
     hipError_t status = hipErrorInvalidValue;
     switch (group) {
-        case 1: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 1>, 64, 0); break;
-        case 2: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 2>, 128, 0); break;
-        case 3: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 3>, 192, 0); break;
-        case 4: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 4>, 256, 0); break;
-        case 5: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 5>, 320, 0); break;
-        case 6: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 6>, 384, 0); break;
-        case 7: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 7>, 448, 0); break;
-        case 8: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 8>, 512, 0); break;
+        case 1: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 1, kPrefillTiles>, 64, 0); break;
+        case 2: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 2, kPrefillTiles>, 128, 0); break;
+        case 3: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 3, kPrefillTiles>, 192, 0); break;
+        case 4: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 4, kPrefillTiles>, 256, 0); break;
+        case 5: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 5, kPrefillTiles>, 320, 0); break;
+        case 6: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 6, kPrefillTiles>, 384, 0); break;
+        case 7: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 7, kPrefillTiles>, 448, 0); break;
+        case 8: status = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, prefill_f16_kernel<D, 8, kPrefillTiles>, 512, 0); break;
         default: break;
     }
     if (status != hipSuccess) {
@@ -495,27 +520,15 @@ int prefill_resident_blocks(int device, int head_dim, int group) {
     return properties.multiProcessorCount * per_cu;
 }
 
-hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int items, bool fp16) {
+hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int first, int items, int tiles, bool fp16) {
     if (items == 0) {
         return hipSuccess;
     }
     if (!fp16) {
         return hipErrorNotSupported;  // the planner sends FP32 prompt runs through the decode kernel
     }
-    const dim3 grid(items);
-    const dim3 block(args.geo.group * 64);
-    // One wave per query head of the group (validated at cache creation: 1..8).
-    switch (args.geo.group) {
-        case 1: return launch_prefill_for<1>(launch, args, grid, block);
-        case 2: return launch_prefill_for<2>(launch, args, grid, block);
-        case 3: return launch_prefill_for<3>(launch, args, grid, block);
-        case 4: return launch_prefill_for<4>(launch, args, grid, block);
-        case 5: return launch_prefill_for<5>(launch, args, grid, block);
-        case 6: return launch_prefill_for<6>(launch, args, grid, block);
-        case 7: return launch_prefill_for<7>(launch, args, grid, block);
-        case 8: return launch_prefill_for<8>(launch, args, grid, block);
-        default: return hipErrorInvalidValue;
-    }
+    return tiles == 1 ? launch_prefill_tiles<1>(launch, args, first, items)
+                      : launch_prefill_tiles<kPrefillTiles>(launch, args, first, items);
 }
 
 }  // namespace synapse_kv

@@ -175,11 +175,12 @@ struct SynapseKvCache {
     synapse_kv::Dims dims{};
     int device = 0;
     hipStream_t stream = nullptr;
-    uint32_t split_keys = 256;  // fewest keys per decode wave worker
+    uint32_t split_keys = 64;  // fewest keys per decode wave worker
     uint32_t prefill_runs = 1;
     uint32_t prefill_split_keys = 0;     // 0: chosen per step (plan_step)
     int32_t prefill_slots = 256;         // resident prefill workgroups on the device
     uint32_t prefetch = 1;  // decode kernel variant: 1 = two register sets, next step's loads in flight
+    uint32_t shared_prefix = 1;  // 1: decode reads copy-on-write pages shared by several step tokens once
 
     // Host shadow of the allocator (same rules as the table kernel).
     std::vector<uint32_t> capacity;
@@ -225,11 +226,14 @@ struct SynapseKvCache {
     int32_t decode_workers = 0;
     int32_t first_level_merges = 0;  // merges[0, first_level_merges) run before the rest
     int32_t merges = 0;
-    int32_t prefill_items = 0;
+    int32_t prefill_items = 0;  // prompt-run items, followed in the blob by listed_items shared-prefix items
+    int32_t listed_items = 0;
+    int32_t listed_tiles = 1;   // column tiles the listed items need (1 when every set has at most 16 members)
     int32_t decode_waves = 1024;  // resident decode waves on the device
     bool fusable = false;         // the step can append and attend in one decode launch
     size_t tokens_offset = 0;
     size_t workers_offset = 0;
+    size_t members_offset = 0;
     size_t segments_offset = 0;
     size_t merges_offset = 0;
     size_t prefill_offset = 0;
@@ -455,26 +459,23 @@ int64_t choose_prefill_chunk(const SynapseKvCache& cache, const SynapseKvBatchTo
 // are not split (and need no merge), short chunks over long caches are.
 void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t count) {
     const Dims& dims = cache.dims;
+    const int32_t group = static_cast<int32_t>(dims.heads / dims.kv_heads);
+    // A row: keys [key_begin, keys) of one (token, KV head), or of a shared set's members (set >= 0, token -1).
     struct Row {
         int32_t token;
         int32_t kv_head;
+        int32_t key_begin;
         int32_t keys;
+        int32_t set;
         int64_t first_step;
         int64_t steps;
+        size_t first_segment;
+        int32_t pieces;
     };
-    std::vector<Row> rows;
     std::vector<PrefillItem> prefill;
     std::vector<MergeItem> prefill_merges;
     int32_t partial_rows = 0;
-    int64_t total_steps = 0;
-    auto add_decode = [&](int32_t index) {
-        const int32_t keys = tokens[index].position + 1;
-        const int64_t steps = (keys + kStepKeys - 1) / kStepKeys;
-        for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
-            rows.push_back(Row{index, static_cast<int32_t>(kv_head), keys, total_steps, steps});
-            total_steps += steps;
-        }
-    };
+    std::vector<int32_t> lone;  // step tokens that go to the decode kernels
     int32_t start = 0;
     std::vector<std::pair<int32_t, int32_t>> runs;
     while (start < count) {
@@ -485,7 +486,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         }
         if (end - start == 1 || cache.prefill_runs == 0 || dims.precision != SYNAPSE_KV_F16) {
             for (int32_t index = start; index < end; ++index) {
-                add_decode(index);
+                lone.push_back(index);
             }
         } else {
             runs.emplace_back(start, end);
@@ -493,20 +494,103 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         start = end;
     }
 
-    // Decode: even split of the flattened steps over the wave workers.
+    // Shared prefixes (FP16): lone tokens whose block tables map their leading pages to the same physical pages
+    // (copy-on-write forks) form sets of up to kPrefillTokens members. A set's shared pages are those all members
+    // map alike, below every member's own position (whose page the step has already made private); listed prefill
+    // items read them once for the whole set, and each member's own keys go through the decode kernel.
+    struct SharedSet {
+        std::vector<int32_t> members;
+        int32_t shared_keys;
+    };
+    std::vector<SharedSet> sets;
+    std::vector<int32_t> set_of(count, -1);
+    if (cache.shared_prefix != 0 && dims.precision == SYNAPSE_KV_F16 && lone.size() > 1) {
+        auto first_page = [&](int32_t index) {
+            return cache.table[static_cast<size_t>(tokens[index].slot) * dims.pages_per_slot];
+        };
+        std::vector<int32_t> order = lone;
+        std::stable_sort(order.begin(), order.end(),
+                         [&](int32_t x, int32_t y) { return first_page(x) < first_page(y); });
+        const size_t most = static_cast<size_t>(kPrefillTokens);
+        for (size_t begin = 0; begin < order.size();) {
+            size_t end = begin + 1;
+            while (end < order.size() && first_page(order[end]) == first_page(order[begin])) {
+                ++end;
+            }
+            if (end - begin > 1 && first_page(order[begin]) >= 0) {
+                const int32_t* reference = &cache.table[static_cast<size_t>(tokens[order[begin]].slot) * dims.pages_per_slot];
+                uint32_t pages = dims.pages_per_slot;
+                for (size_t k = begin; k < end; ++k) {
+                    const int32_t* table = &cache.table[static_cast<size_t>(tokens[order[k]].slot) * dims.pages_per_slot];
+                    uint32_t same = 0;
+                    const uint32_t below = static_cast<uint32_t>(tokens[order[k]].position) / dims.page_tokens;
+                    while (same < std::min(pages, below) && table[same] == reference[same]) {
+                        ++same;
+                    }
+                    pages = same;
+                }
+                for (size_t first = begin; pages > 0 && first < end; first += most) {
+                    const size_t last = std::min(end, first + most);
+                    if (last - first < 2) {
+                        continue;
+                    }
+                    SharedSet set{std::vector<int32_t>(order.begin() + first, order.begin() + last),
+                                  static_cast<int32_t>(pages * dims.page_tokens)};
+                    std::sort(set.members.begin(), set.members.end());
+                    for (int32_t member : set.members) {
+                        set_of[member] = static_cast<int32_t>(sets.size());
+                    }
+                    sets.push_back(std::move(set));
+                }
+            }
+            begin = end;
+        }
+    }
+
+    // Rows: every lone token's (token, KV head) rows, from the token's shared keys on.
+    std::vector<Row> rows;
+    for (int32_t index : lone) {
+        const int32_t keys = tokens[index].position + 1;
+        const int32_t key_begin = set_of[index] >= 0 ? sets[set_of[index]].shared_keys : 0;
+        for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
+            rows.push_back(Row{index, static_cast<int32_t>(kv_head), key_begin, keys, set_of[index], 0,
+                               (keys - key_begin + kStepKeys - 1) / kStepKeys, 0, 0});
+        }
+    }
+
+    // Even split: the steps of all rows laid end to end, cut into equal shares for the resident wave workers (at
+    // least split_keys keys each). A row cut by worker boundaries becomes several segments.
     std::vector<DecodeSegment> segments;
-    std::vector<int32_t> worker_segments;
-    std::vector<MergeItem> merges;
-    int32_t workers = 0;
-    if (total_steps > 0) {
-        const int64_t per_worker_min = std::max<int64_t>(1, cache.split_keys / kStepKeys);
+    auto split = [&](std::vector<Row>& list, int32_t resident, std::vector<int32_t>& worker_segments) -> int32_t {
+        int64_t total_steps = 0;
+        for (Row& row : list) {
+            row.first_step = total_steps;
+            total_steps += row.steps;
+        }
+        if (total_steps == 0) {
+            return 0;
+        }
+        // Each worker takes at least split_keys keys. When a row would still be cut into more than 64 pieces (a
+        // second merge launch), workers take enough steps to avoid that if it costs at most kMergeSteps more steps
+        // each (about one merge launch of latency).
+        int64_t longest = 0;
+        for (const Row& row : list) {
+            longest = std::max(longest, row.steps);
+        }
+        int64_t per_worker_min = std::max<int64_t>(1, cache.split_keys / kStepKeys);
+        const int64_t filled = std::max(per_worker_min, (total_steps + resident - 1) / resident);
+        const int64_t single_level = (longest + 62) / 63;
+        if (single_level > filled && single_level - filled <= kMergeSteps) {
+            per_worker_min = single_level;
+        }
         const int64_t wanted = std::max<int64_t>(1, total_steps / per_worker_min);
-        workers = static_cast<int32_t>(std::min<int64_t>(std::min<int64_t>(wanted, cache.decode_waves), total_steps));
+        const int32_t workers =
+            static_cast<int32_t>(std::min<int64_t>(std::min<int64_t>(wanted, resident), total_steps));
         auto boundary = [&](int64_t worker) { return worker * total_steps / workers; };
         int64_t worker = 0;
-        worker_segments.push_back(0);
-        for (const Row& row : rows) {
-            const size_t first_segment = segments.size();
+        worker_segments.push_back(static_cast<int32_t>(segments.size()));
+        for (Row& row : list) {
+            row.first_segment = segments.size();
             const int64_t row_end = row.first_step + row.steps;
             int64_t step = row.first_step;
             while (step < row_end) {
@@ -515,25 +599,89 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
                     worker_segments.push_back(static_cast<int32_t>(segments.size()));
                 }
                 const int64_t stop = std::min<int64_t>(row_end, boundary(worker + 1));
-                const int32_t key_begin = static_cast<int32_t>((step - row.first_step) * kStepKeys);
+                const int32_t key_begin = row.key_begin + static_cast<int32_t>((step - row.first_step) * kStepKeys);
                 const int32_t key_end =
-                    std::min<int32_t>(row.keys, static_cast<int32_t>((stop - row.first_step) * kStepKeys));
+                    std::min<int32_t>(row.keys, row.key_begin + static_cast<int32_t>((stop - row.first_step) * kStepKeys));
                 segments.push_back(DecodeSegment{row.token, row.kv_head, key_begin, key_end, -1, -1, {0, 0}});
                 step = stop;
             }
-            const int32_t pieces = static_cast<int32_t>(segments.size() - first_segment);
-            if (pieces > 1) {
-                const int32_t merge = static_cast<int32_t>(merges.size());
-                merges.push_back(MergeItem{row.token, row.kv_head, partial_rows, pieces, -1, {0, 0, 0}});
-                for (int32_t piece = 0; piece < pieces; ++piece) {
-                    segments[first_segment + piece].row = partial_rows + piece;
-                    segments[first_segment + piece].merge = merge;
-                }
-                partial_rows += pieces;
-            }
+            row.pieces = static_cast<int32_t>(segments.size() - row.first_segment);
         }
         while (static_cast<int32_t>(worker_segments.size()) < workers + 1) {
             worker_segments.push_back(static_cast<int32_t>(segments.size()));
+        }
+        return workers;
+    };
+    std::vector<int32_t> worker_segments;
+    const int32_t workers = split(rows, cache.decode_waves, worker_segments);
+
+    // Partial rows and merge entries. A row of its own that was cut gets consecutive partial rows. A shared set's
+    // keys are cut, per KV head, into P listed prefill items of about equal length (enough items over all sets to
+    // fill the device's prefill workgroup slots, at least kMinSharedSteps steps each). With Q_m own pieces of
+    // member m, member m owns the rows base + m * stride .. + P + Q_m - 1 (stride = P + max Q_m): its shared
+    // pieces first, then its own.
+    std::vector<MergeItem> merges;
+    std::vector<int32_t> members;
+    for (const Row& row : rows) {
+        if (row.set >= 0 || row.pieces < 2) {
+            continue;
+        }
+        const int32_t merge = static_cast<int32_t>(merges.size());
+        merges.push_back(MergeItem{row.token, row.kv_head, partial_rows, row.pieces, -1, {0, 0, 0}});
+        for (int32_t piece = 0; piece < row.pieces; ++piece) {
+            segments[row.first_segment + piece].row = partial_rows + piece;
+            segments[row.first_segment + piece].merge = merge;
+        }
+        partial_rows += row.pieces;
+    }
+    std::vector<PrefillItem> listed;
+    int32_t listed_tiles = 1;
+    if (!sets.empty()) {
+        // own_rows[token * kv_heads + kv_head]: the row of a set member's own keys.
+        std::vector<const Row*> own_rows(static_cast<size_t>(count) * dims.kv_heads, nullptr);
+        for (const Row& row : rows) {
+            if (row.set >= 0) {
+                own_rows[static_cast<size_t>(row.token) * dims.kv_heads + row.kv_head] = &row;
+            }
+        }
+        int64_t shared_steps = 0;
+        for (const SharedSet& set : sets) {
+            shared_steps += static_cast<int64_t>(dims.kv_heads) * (set.shared_keys / kStepKeys);
+        }
+        const int64_t item_steps =
+            std::max<int64_t>(kMinSharedSteps, (shared_steps + cache.prefill_slots - 1) / cache.prefill_slots);
+        for (const SharedSet& set : sets) {
+            const int32_t offset = static_cast<int32_t>(members.size());
+            members.insert(members.end(), set.members.begin(), set.members.end());
+            const int32_t size = static_cast<int32_t>(set.members.size());
+            listed_tiles = std::max(listed_tiles, (size + 15) / 16);
+            const int64_t steps = set.shared_keys / kStepKeys;
+            const int32_t pieces = static_cast<int32_t>((steps + item_steps - 1) / item_steps);
+            for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
+                int32_t most_own = 0;
+                for (int32_t member : set.members) {
+                    most_own = std::max(most_own, own_rows[static_cast<size_t>(member) * dims.kv_heads + kv_head]->pieces);
+                }
+                const int32_t stride = pieces + most_own;
+                const int32_t base = partial_rows;
+                partial_rows += size * stride;
+                for (int32_t piece = 0; piece < pieces; ++piece) {
+                    const int32_t begin = static_cast<int32_t>(piece * steps / pieces * kStepKeys);
+                    const int32_t finish = static_cast<int32_t>((piece + 1) * steps / pieces * kStepKeys);
+                    listed.push_back(PrefillItem{offset, size, static_cast<int32_t>(kv_head), begin, finish, base + piece,
+                                                 stride, 1});
+                }
+                for (int32_t m = 0; m < size; ++m) {
+                    const Row& own = *own_rows[static_cast<size_t>(set.members[m]) * dims.kv_heads + kv_head];
+                    const int32_t merge = static_cast<int32_t>(merges.size());
+                    merges.push_back(MergeItem{own.token, own.kv_head, base + m * stride, pieces + own.pieces, -1,
+                                               {0, 0, 0}});
+                    for (int32_t piece = 0; piece < own.pieces; ++piece) {
+                        segments[own.first_segment + piece].row = base + m * stride + pieces + piece;
+                        segments[own.first_segment + piece].merge = merge;
+                    }
+                }
+            }
         }
     }
 
@@ -575,6 +723,9 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             }
         }
     }
+    // Prompt-run items first, then the listed items (a launch of their own when one column tile holds every set).
+    const int32_t prompt_items = static_cast<int32_t>(prefill.size());
+    prefill.insert(prefill.end(), listed.begin(), listed.end());
     merges.insert(merges.end(), prefill_merges.begin(), prefill_merges.end());
     // Merges over more than 64 partial rows first combine blocks of 64 rows into intermediate partial rows (one
     // launch), then merge those (a second launch); the merge kernel's single load round covers 64 rows.
@@ -601,17 +752,18 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     const size_t tokens_bytes = static_cast<size_t>(count) * sizeof(SynapseKvBatchToken);
     cache.tokens_offset = 0;
     cache.workers_offset = align_up(tokens_bytes, 256);
-    cache.segments_offset = align_up(cache.workers_offset + worker_segments.size() * sizeof(int32_t), 256);
+    cache.members_offset = align_up(cache.workers_offset + worker_segments.size() * sizeof(int32_t), 256);
+    cache.segments_offset = align_up(cache.members_offset + members.size() * sizeof(int32_t), 256);
     cache.merges_offset = align_up(cache.segments_offset + segments.size() * sizeof(DecodeSegment), 256);
     cache.prefill_offset = align_up(cache.merges_offset + merges.size() * sizeof(MergeItem), 256);
     const size_t total = cache.prefill_offset + prefill.size() * sizeof(PrefillItem);
     cache.blob.ensure(total, "step buffer");
-    const size_t group = dims.heads / dims.kv_heads;
     cache.partial_out.ensure(static_cast<size_t>(partial_rows) * group * dims.head_dim, "attention partials");
     cache.partial_ml.ensure(static_cast<size_t>(partial_rows) * group * 2, "attention partial statistics");
     auto* staging = static_cast<uint8_t*>(cache.uploader.acquire(total));
     std::memcpy(staging + cache.tokens_offset, tokens, tokens_bytes);
     std::memcpy(staging + cache.workers_offset, worker_segments.data(), worker_segments.size() * sizeof(int32_t));
+    std::memcpy(staging + cache.members_offset, members.data(), members.size() * sizeof(int32_t));
     std::memcpy(staging + cache.segments_offset, segments.data(), segments.size() * sizeof(DecodeSegment));
     std::memcpy(staging + cache.merges_offset, merges.data(), merges.size() * sizeof(MergeItem));
     std::memcpy(staging + cache.prefill_offset, prefill.data(), prefill.size() * sizeof(PrefillItem));
@@ -620,15 +772,19 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.decode_workers = workers;
     cache.first_level_merges = first_level_merges;
     cache.merges = static_cast<int32_t>(merges.size());
-    cache.prefill_items = static_cast<int32_t>(prefill.size());
-    // The fused append + decode launch needs every token to own its slot: no token may read another token's
-    // position of the same step, and each (token, KV head) row appends its own position only.
+    cache.prefill_items = prompt_items;
+    cache.listed_items = static_cast<int32_t>(listed.size());
+    cache.listed_tiles = listed_tiles;
+    // The fused append + decode launch needs every token to own its slot (no token may read another token's
+    // position of the same step, and each (token, KV head) row appends its own position only) and no prompt run
+    // (whose K/V must be in the pages before its attention); listed items read only pages below every member's
+    // position.
     std::vector<int32_t> slots(count);
     for (int32_t index = 0; index < count; ++index) {
         slots[index] = tokens[index].slot;
     }
     std::sort(slots.begin(), slots.end());
-    cache.fusable = prefill.empty() && std::adjacent_find(slots.begin(), slots.end()) == slots.end();
+    cache.fusable = prompt_items == 0 && std::adjacent_find(slots.begin(), slots.end()) == slots.end();
     cache.step_ready = true;
 }
 
@@ -870,15 +1026,27 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
     args.sines = cache.sines.pointer;
     args.workers = cache.decode_workers;
     args.worker_segments = reinterpret_cast<const int32_t*>(cache.blob.pointer + cache.workers_offset);
+    args.members = reinterpret_cast<const int32_t*>(cache.blob.pointer + cache.members_offset);
     args.segments = reinterpret_cast<const DecodeSegment*>(cache.blob.pointer + cache.segments_offset);
     args.merges = reinterpret_cast<const MergeItem*>(cache.blob.pointer + cache.merges_offset);
     args.prefill = reinterpret_cast<const PrefillItem*>(cache.blob.pointer + cache.prefill_offset);
     args.partial_out = cache.partial_out.pointer;
     args.partial_ml = cache.partial_ml.pointer;
     const bool fp16 = dims.precision == SYNAPSE_KV_F16;
-    check_hip(launch_prefill(launch_for(cache, SYNAPSE_KV_KERNEL_PREFILL, cache.prefill_items > 0), args,
-                             cache.prefill_items, fp16),
-              "prefill attention");
+    const int prompt_items = cache.prefill_items;
+    const int listed_items = cache.listed_items;
+    if (cache.listed_tiles == 1) {
+        check_hip(launch_prefill(launch_for(cache, SYNAPSE_KV_KERNEL_PREFILL, prompt_items > 0), args, 0, prompt_items,
+                                 kPrefillTiles, fp16),
+                  "prefill attention");
+        check_hip(launch_prefill(launch_for(cache, SYNAPSE_KV_KERNEL_PREFILL, listed_items > 0), args, prompt_items,
+                                 listed_items, 1, fp16),
+                  "shared-prefix attention");
+    } else {
+        check_hip(launch_prefill(launch_for(cache, SYNAPSE_KV_KERNEL_PREFILL, prompt_items + listed_items > 0), args, 0,
+                                 prompt_items + listed_items, kPrefillTiles, fp16),
+                  "prefill attention");
+    }
     check_hip(launch_decode(launch_for(cache, SYNAPSE_KV_KERNEL_DECODE, args.workers > 0), args, fp16, cache.prefetch != 0),
               "decode attention");
     const int first_level = cache.first_level_merges;
@@ -976,6 +1144,8 @@ int32_t synapse_kv_set_option(SynapseKvCache* cache, uint32_t option, uint32_t v
             cache->prefetch = value != 0 ? 1 : 0;
             cache->decode_waves = decode_resident_waves(cache->device, cache->dims.precision == SYNAPSE_KV_F16,
                                                         cache->dims.head_dim, cache->prefetch != 0);
+        } else if (option == SYNAPSE_KV_OPTION_SHARED_PREFIX) {
+            cache->shared_prefix = value != 0 ? 1 : 0;
         } else if (option == SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS) {
             if (value % kStepKeys != 0) {
                 invalid("prefill split keys must be 0 (automatic) or a multiple of 64");

@@ -76,10 +76,13 @@ struct MergeItem {
     int32_t pad[3];
 };
 
-// A prefill work item: `count` (<= kPrefillTokens) consecutive tokens of one prompt run (consecutive positions of
-// one slot) starting at step token `first_token`, every query head of `kv_head`, keys [key_begin, key_end).
-// `row` >= 0: token j of the item writes partial row `row + j * row_stride` (the decode merge layout);
-// -1: the normalized output is written directly.
+// A prefill work item: every query head of `kv_head` over keys [key_begin, key_end) for `count` (<= kPrefillTokens)
+// columns. With listed == 0 the columns are consecutive tokens of one prompt run (consecutive positions of one
+// slot) starting at step token `first_token`, masked causally. With listed == 1 they are the step tokens
+// members[first_token .. first_token + count - 1], whose block tables all map the item's keys to the same pages
+// (a copy-on-write prefix below every member's position): no mask, each column rotated at its own position.
+// `row` >= 0: column j writes partial row `row + j * row_stride` (the decode merge layout); -1: the normalized
+// output is written directly.
 struct PrefillItem {
     int32_t first_token;
     int32_t count;
@@ -88,7 +91,7 @@ struct PrefillItem {
     int32_t key_end;
     int32_t row;
     int32_t row_stride;
-    int32_t pad;
+    int32_t listed;
 };
 static_assert(sizeof(PrefillItem) == 32, "PrefillItem is 32 bytes");
 
@@ -132,6 +135,7 @@ struct AttentionArgs {
     int32_t workers;                 // decode wave workers
     const int32_t* worker_segments;  // [workers + 1]: worker w walks segments [ws[w], ws[w + 1])
     const DecodeSegment* segments;
+    const int32_t* members;  // step token indices of listed prefill items' columns
     const MergeItem* merges;
     const PrefillItem* prefill;
     float* partial_out;  // [rows][group][head_dim]
@@ -171,7 +175,8 @@ hipError_t launch_merge(const Launch& launch, const AttentionArgs& args, int fir
 int decode_resident_waves(int device, bool fp16, int head_dim, bool prefetch);
 // Prefill workgroups resident on the whole device at once (occupancy of the group's kernel times the CU count).
 int prefill_resident_blocks(int device, int head_dim, int group);
-hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int items, bool fp16);
+// Prefill items [first, first + items) with `tiles` (1 or kPrefillTiles) column tiles of 16 tokens per wave.
+hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int first, int items, int tiles, bool fp16);
 hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16);
 
 // Query rows (tokens) per prefill work item: 16 per MFMA column tile, kPrefillTiles tiles per wave.
@@ -181,5 +186,9 @@ constexpr int kPrefillTokens = 16 * kPrefillTiles;
 constexpr int kStepKeys = 64;
 // Fewest keys per prefill work item when the split is chosen automatically.
 constexpr int kMinPrefillChunk = 1024;
+// Decode steps per worker that one merge launch is worth (the planner adds up to this many to avoid a second).
+constexpr int kMergeSteps = 4;
+// Fewest 64-key steps per listed (shared-prefix) prefill item.
+constexpr int kMinSharedSteps = 4;
 
 }  // namespace synapse_kv

@@ -35,6 +35,7 @@ OPTION_PREFILL_RUNS = 2
 OPTION_PREFILL_SPLIT_KEYS = 3
 OPTION_DECODE_PREFETCH = 4
 OPTION_PROFILE_EVERY = 5
+OPTION_SHARED_PREFIX = 6
 
 
 class SynapseKvError(RuntimeError):

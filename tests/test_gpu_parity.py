@@ -191,8 +191,9 @@ def test_append_attention_matches_the_restatement(torch_gpu, heads, kv_heads, he
 
 
 def test_rows_cut_into_many_pieces(torch_gpu):
-    """Rows of 79 and 2 64-key steps with one step per worker: the long rows' 79 partials go through the two-level
-    merge (blocks of 64 partial rows, then the blocks); three layers reuse one plan."""
+    """A 79-step decode row cut as finely as the planner allows (at most 64 pieces, one merge launch), and a prompt
+    chunk over the same cache with 64-key prefill pieces: 79 partial rows per token, merged in two levels (blocks
+    of 64 partial rows, then the blocks). Three layers reuse each plan."""
     say("many pieces")
     pair = Pair(torch_gpu, heads=28, kv_heads=4, head_dim=128, max_positions=8192, growth=1024, max_pages=40,
                 layers=3, slots=2)
@@ -205,6 +206,8 @@ def test_rows_cut_into_many_pieces(torch_gpu):
         pair.gpu.set_split_keys(split)
         assert pair.step([(slot, lengths[slot]) for slot in range(2)], rng, fused=fused) == 0
         lengths = [length + 1 for length in lengths]
+    pair.gpu.set_prefill_split_keys(64)
+    assert pair.step([(0, p) for p in range(lengths[0], lengths[0] + 20)], rng) == 0
     pair.check_contents(0)
 
 
@@ -298,6 +301,35 @@ def test_copy_on_write_keeps_both_histories(torch_gpu):
     assert pair.step([(0, 150), (1, 151), (2, 151), (3, 151)], rng) == 0
     pair.check_tables()
     for slot in range(4):
+        pair.check_contents(slot)
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(28, 4, 128), (14, 2, 64), (8, 8, 128)])
+def test_forks_read_shared_pages_once(torch_gpu, heads, kv_heads, head_dim):
+    """A 700-token prefix forked into 10 slots: the 11 decode tokens share pages 0..9 copy-on-write, so the shared
+    kernel attends those 640 keys once per set of members (8 + 3 under GQA 7:1, one set of 11 otherwise) and the
+    merge joins each member's own keys; outputs are checked against the restatement with the shared path on and
+    off, split and unsplit, through append_rope + attention and through append_attention."""
+    from synapse_amd.native import OPTION_SHARED_PREFIX
+
+    say("shared prefix decode", heads, kv_heads, head_dim)
+    pair = Pair(torch_gpu, heads=heads, kv_heads=kv_heads, head_dim=head_dim, page=64, growth=64,
+                max_positions=2048, slots=12, max_pages=160)
+    rng = np.random.default_rng(head_dim + heads)
+    for first in range(0, 700, 256):
+        assert pair.step([(0, p) for p in range(first, min(700, first + 256))], rng, attend=False) == 0
+    for target in range(1, 11):
+        pair.call("fork", 0, target)
+    position = 700
+    for shared, split, fused in ((1, 256, False), (1, 64, True), (0, 256, True), (1, 512, True), (1, 128, False)):
+        pair.gpu.set_option(OPTION_SHARED_PREFIX, shared)
+        pair.gpu.set_split_keys(split)
+        assert pair.step([(slot, position) for slot in range(11)], rng, fused=fused) == 0
+        position += 1
+    # Ragged: only some forks advance, and one slot holds two lone tokens of the step.
+    assert pair.step([(3, position), (5, position), (5, position + 2), (9, position)], rng) == 0
+    pair.check_tables()
+    for slot in range(11):
         pair.check_contents(slot)
 
 
