@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 /* ABI version checked by the loader before any other call (ffi.rs:12 ABI_VERSION; NativeGpuLibrary.cs:14). */
-#define SYNAPSE_KV_ABI_VERSION 1u
+#define SYNAPSE_KV_ABI_VERSION 2u
 
 /* Status codes, identical to error.rs:4-16. */
 #define SYNAPSE_KV_OK 0
@@ -216,6 +216,65 @@ int32_t synapse_kv_read_kv(SynapseKvCache* cache, uint32_t slot, uint32_t layer,
 int32_t synapse_kv_rope_table(uint32_t head_dim, float theta, float yarn_factor, uint32_t yarn_original,
                               uint32_t positions, float* cosines, float* sines);
 
+/* ---- Q8_0 projections: the QKV and o_proj matrices that feed and consume the attention path ----
+ * synapse_q8_matvec_{1,2,4,8} and synapse_q8_gemm (cuda/kernels/matmul.cu:1-189, metal/shaders/matmul.metal:1-310;
+ * host step/projection.rs:1-141). Weights are GGML Q8_0 rows (34-byte blocks: FP16 scale d, then 32 int8 codes;
+ * element = d * code) at byte offsets of a host blob (the mapped model file, GpuLayoutMapping.cs:14-32), with
+ * optional FP32 biases. Activations and results are FP32 and every product accumulates in FP32 (ADR-012). */
+
+/* No bias for a matrix (SYNAPSE_NO_BIAS, common.metal:11). */
+#define SYNAPSE_KV_NO_BIAS UINT64_MAX
+
+/* One matrix of the blob (the weight/bias/rows fields of matmul_segment, common.metal:54-59). */
+typedef struct SynapseKvMatrix {
+    uint64_t weight;  /* byte offset of rows x (columns / 32) Q8_0 blocks, row-major */
+    uint64_t bias;    /* byte offset of `rows` FP32 biases, or SYNAPSE_KV_NO_BIAS */
+    uint32_t rows;    /* positive */
+    uint32_t columns; /* a positive multiple of 32 */
+} SynapseKvMatrix;
+
+typedef struct SynapseKvWeights SynapseKvWeights;
+
+/* Uploads `count` matrices of a host blob to the current HIP device in the kernels' layout: 16-row x 64-column
+ * tiles of codes in MFMA fragment order with their FP16 scales beside them, padded with zero codes (the weight
+ * upload of synapse_gpu_decoder_create, ffi.rs:106-142, for the projection matrices). The blob is not kept. */
+int32_t synapse_kv_weights_create(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMatrix* matrices,
+                                  uint32_t count, SynapseKvWeights** weights);
+
+/* Null is ignored. */
+void synapse_kv_weights_destroy(SynapseKvWeights* weights);
+
+/* Device bytes held by the weights; 0 for null. */
+uint64_t synapse_kv_weights_bytes(const SynapseKvWeights* weights);
+
+/* Orders the projections on `stream` (a hipStream_t; null = the default stream). */
+int32_t synapse_kv_weights_set_stream(SynapseKvWeights* weights, void* stream);
+
+/* One projection (matmul_args, common.metal:61-71): the rows of up to three matrices with equal column counts,
+ * in order (e.g. Q, K and V), matrix s written to output columns out_column[s] + row:
+ *   output[t][out_column[s] + row] = (accumulate ? output[t][...] : 0) + sum_k W_s[row][k] * input[t][k] + bias_s[row]
+ * for tokens t < tokens (accumulate adds the residual, as o_proj does, step/layers.rs:96-108). */
+typedef struct SynapseKvProjection {
+    uint32_t matrix[3];     /* matrix indices of synapse_kv_weights_create */
+    uint32_t out_column[3]; /* first output column of each matrix's rows */
+    uint32_t segments;      /* 1..3 */
+    uint32_t tokens;        /* positive */
+    uint32_t in_stride;     /* floats between input rows, at least columns */
+    uint32_t out_stride;    /* floats between output rows */
+    uint32_t accumulate;    /* 0 or 1 */
+    uint32_t reserved;      /* 0 */
+} SynapseKvProjection;
+
+/* Runs a projection on the weights' stream (the matrix-vector kernel for decode tokens and the tiled GEMM for
+ * prompt runs, project() in step/projection.rs:51-72, as one MFMA kernel); input and output are device pointers.
+ * Output rows of different tokens must not overlap the input. */
+int32_t synapse_kv_project(SynapseKvWeights* weights, const SynapseKvProjection* projection, const float* input,
+                           float* output);
+
+/* Copies matrix `index` back in GGML Q8_0 block order (rows x columns / 32 blocks of 34 bytes) into host memory of
+ * at least that many bytes (read-back for checks). */
+int32_t synapse_kv_weights_read(SynapseKvWeights* weights, uint32_t index, uint8_t* blocks, uint64_t bytes);
+
 #ifdef __cplusplus
 } /* extern "C" */
 
@@ -224,12 +283,16 @@ static_assert(sizeof(SynapseKvBatchToken) == 16, "SynapseKvBatchToken is pinned 
 static_assert(sizeof(SynapseKvDesc) == 64, "SynapseKvDesc is pinned at 64 bytes");
 static_assert(sizeof(SynapseKvPageStats) == 40, "SynapseKvPageStats is pinned at 40 bytes");
 static_assert(sizeof(SynapseKvProfile) == 128, "SynapseKvProfile is pinned at 128 bytes");
+static_assert(sizeof(SynapseKvMatrix) == 24, "SynapseKvMatrix is pinned at 24 bytes");
+static_assert(sizeof(SynapseKvProjection) == 48, "SynapseKvProjection is pinned at 48 bytes");
 #else
 _Static_assert(sizeof(SynapseKvDeviceInfo) == 152, "SynapseKvDeviceInfo is pinned at 152 bytes");
 _Static_assert(sizeof(SynapseKvBatchToken) == 16, "SynapseKvBatchToken is pinned at 16 bytes");
 _Static_assert(sizeof(SynapseKvDesc) == 64, "SynapseKvDesc is pinned at 64 bytes");
 _Static_assert(sizeof(SynapseKvPageStats) == 40, "SynapseKvPageStats is pinned at 40 bytes");
 _Static_assert(sizeof(SynapseKvProfile) == 128, "SynapseKvProfile is pinned at 128 bytes");
+_Static_assert(sizeof(SynapseKvMatrix) == 24, "SynapseKvMatrix is pinned at 24 bytes");
+_Static_assert(sizeof(SynapseKvProjection) == 48, "SynapseKvProjection is pinned at 48 bytes");
 #endif
 
 #endif /* SYNAPSE_KV_H */

@@ -3,7 +3,7 @@
 // loads or calls this file. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use it.
 //
 // Every function cites the reference file:line it restates (paths relative to the managedcode/Synapse tree).
-// Pinning (how each part is checked against something other than itself) is listed in oracle/README.md.
+// Pinning (how each part is checked against something other than itself) is in tests/test_oracle_*.py.
 //
 // Build: oracle/Makefile (g++ -O3 -ffp-contract=off; no fast-math, so float expressions round exactly as the
 // reference's C# does: one rounding per operation, no fused multiply-add).
@@ -1040,6 +1040,132 @@ double orc_paged_attention(void* handle, int layer, const float* qkv, int qkv_st
                        output + static_cast<size_t>(index) * out_stride + static_cast<size_t>(head) * d);
     });
     return std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+}
+
+// ---- Q8_0 projections ---------------------------------------------------------------------------------------
+
+// One matrix of a projection: GGML Q8_0 rows (34-byte blocks: FP16 d, 32 int8 codes; common.metal:13-16) at
+// `weight`, optional FP32 biases, and the first output column (matmul_segment, common.metal:54-59).
+struct Q8Segment {
+    const uint8_t* weight;
+    const float* bias;  // null: none
+    int rows;
+    int out_column;
+};
+
+static float q8_scale(const uint8_t* block) {
+    uint16_t bits;
+    std::memcpy(&bits, block, 2);
+    return f16_to_f32(bits);
+}
+
+// dot8 (matmul.cu:7-17): eight codes times eight activations, an explicit fma chain from the left.
+static float q8_dot8(const int8_t* q, const float* x) {
+    float acc = static_cast<float>(q[0]) * x[0];
+    for (int i = 1; i < 8; ++i) {
+        acc = std::fma(static_cast<float>(q[i]), x[i], acc);
+    }
+    return acc;
+}
+
+// q8_matvec<T> + matvec_finish (matmul.cu:45-111) for one (row, token): four warps of 32 lanes; lane l of warp w
+// takes quarter l % 4 of blocks w * 8 + l / 4, w * 8 + l / 4 + 32, ...; sum = fma(dot8, d, sum); warp_sum
+// (common.cuh:127-133: value += shfl_xor(value, 16, 8, 4, 2, 1)); the warps' totals added in order; then the bias.
+static float q8_matvec_row(const uint8_t* row, int blocks, const float* x) {
+    float warp_total[4];
+    for (int warp = 0; warp < 4; ++warp) {
+        float lane[32];
+        for (int l = 0; l < 32; ++l) {
+            float sum = 0.0f;
+            const int quarter = l % 4;
+            for (int block = warp * 8 + l / 4; block < blocks; block += 32) {
+                const uint8_t* b = row + static_cast<size_t>(block) * 34;
+                sum = std::fma(q8_dot8(reinterpret_cast<const int8_t*>(b + 2 + quarter * 8), x + block * 32 + quarter * 8),
+                               q8_scale(b), sum);
+            }
+            lane[l] = sum;
+        }
+        for (int offset = 16; offset > 0; offset >>= 1) {
+            float next[32];
+            for (int l = 0; l < 32; ++l) {
+                next[l] = lane[l] + lane[l ^ offset];
+            }
+            std::memcpy(lane, next, sizeof(lane));
+        }
+        warp_total[warp] = lane[0];
+    }
+    return ((warp_total[0] + warp_total[1]) + warp_total[2]) + warp_total[3];
+}
+
+// The reference's FP32 matrix-vector projection (matmul.cu:45-118) on `threads` std::threads over rows: output
+// [t][out_column + row] = (accumulate ? output : 0) + (matvec sum + bias). Returns the wall time in seconds.
+double orc_q8_project_f32(const uint8_t* const* weights, const float* const* biases, const int* rows,
+                          const int* out_columns, int segments, int columns, int tokens, const float* input,
+                          int in_stride, float* output, int out_stride, int accumulate, int threads) {
+    const int blocks = columns / 32;
+    std::vector<Q8Segment> list;
+    int total_rows = 0;
+    for (int s = 0; s < segments; ++s) {
+        list.push_back(Q8Segment{weights[s], biases[s], rows[s], out_columns[s]});
+        total_rows += rows[s];
+    }
+    const auto start = std::chrono::steady_clock::now();
+    Pool::run(total_rows, std::max(1, threads), [&](int, int item) {
+        int local = item;
+        size_t s = 0;
+        while (s + 1 < list.size() && local >= list[s].rows) {  // locate_segment (common.metal:138-146)
+            local -= list[s].rows;
+            ++s;
+        }
+        const Q8Segment& seg = list[s];
+        const uint8_t* row = seg.weight + static_cast<size_t>(local) * blocks * 34;
+        for (int t = 0; t < tokens; ++t) {
+            float total = q8_matvec_row(row, blocks, input + static_cast<size_t>(t) * in_stride);
+            if (seg.bias != nullptr) {
+                total += seg.bias[local];
+            }
+            float& destination = output[static_cast<size_t>(t) * out_stride + seg.out_column + local];
+            destination = accumulate != 0 ? destination + total : total;
+        }
+    });
+    return std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+}
+
+// The same projection accumulated in FP64 and rounded once (the tolerance anchor): output = (accumulate ? output
+// : 0) + sum_k d * code * x + bias. `magnitude` (optional, [tokens][out_stride]) receives sum_k |d * code * x|
+// + |bias| per written element, the scale of FP32 summation error.
+void orc_q8_project_f64(const uint8_t* const* weights, const float* const* biases, const int* rows,
+                        const int* out_columns, int segments, int columns, int tokens, const float* input, int in_stride,
+                        float* output, int out_stride, int accumulate, double* magnitude) {
+    const int blocks = columns / 32;
+    for (int s = 0; s < segments; ++s) {
+        for (int row = 0; row < rows[s]; ++row) {
+            const uint8_t* w = weights[s] + static_cast<size_t>(row) * blocks * 34;
+            for (int t = 0; t < tokens; ++t) {
+                const float* x = input + static_cast<size_t>(t) * in_stride;
+                double sum = 0.0;
+                double size = 0.0;
+                for (int block = 0; block < blocks; ++block) {
+                    const double d = q8_scale(w + static_cast<size_t>(block) * 34);
+                    const int8_t* q = reinterpret_cast<const int8_t*>(w + static_cast<size_t>(block) * 34 + 2);
+                    for (int i = 0; i < 32; ++i) {
+                        const double term = d * q[i] * static_cast<double>(x[block * 32 + i]);
+                        sum += term;
+                        size += std::fabs(term);
+                    }
+                }
+                if (biases[s] != nullptr) {
+                    sum += biases[s][row];
+                    size += std::fabs(static_cast<double>(biases[s][row]));
+                }
+                const size_t at = static_cast<size_t>(t) * out_stride + out_columns[s] + row;
+                output[at] = static_cast<float>(accumulate != 0 ? static_cast<double>(output[at]) + sum : sum);
+                if (magnitude != nullptr) {
+                    magnitude[at] = size + (accumulate != 0 ? std::fabs(static_cast<double>(output[at])) : 0.0);
+                }
+            }
+        }
+    }
 }
 
 // ---- Schedule -------------------------------------------------------------------------------------------------

@@ -14,51 +14,11 @@
 #include <string>
 #include <vector>
 
+#include "abi_support.h"
 #include "kv_internal.h"
 
 namespace synapse_kv {
 namespace {
-
-thread_local std::string g_last_error;
-
-struct Failure {
-    int32_t status;
-    std::string message;
-};
-
-[[noreturn]] void fail(int32_t status, const std::string& message) { throw Failure{status, message}; }
-
-[[noreturn]] void invalid(const std::string& message) { fail(SYNAPSE_KV_INVALID_ARGUMENT, "invalid argument: " + message); }
-
-void check_hip(hipError_t error, const char* what) {
-    if (error == hipSuccess) {
-        return;
-    }
-    const int32_t status = error == hipErrorOutOfMemory ? SYNAPSE_KV_OUT_OF_MEMORY : SYNAPSE_KV_DEVICE_ERROR;
-    fail(status, std::string(status == SYNAPSE_KV_OUT_OF_MEMORY ? "out of device memory: " : "device error: ") + what +
-                     ": " + hipGetErrorString(error));
-}
-
-int32_t record(int32_t status, const std::string& message) {
-    g_last_error = message;
-    return status;
-}
-
-template <typename Body>
-int32_t guarded(Body body) {
-    try {
-        body();
-        return SYNAPSE_KV_OK;
-    } catch (const Failure& failure) {
-        return record(failure.status, failure.message);
-    } catch (const std::bad_alloc&) {
-        return record(SYNAPSE_KV_OUT_OF_MEMORY, "out of host memory");
-    } catch (const std::exception& error) {
-        return record(SYNAPSE_KV_PANIC, std::string("a C++ exception was caught at the KV ABI: ") + error.what());
-    } catch (...) {
-        return record(SYNAPSE_KV_PANIC, "a C++ exception was caught at the KV ABI");
-    }
-}
 
 // Qwen2KvCache.NextCapacity (Qwen2KvCache.cs:91-95) = DecoderShape::next_capacity (decoder.rs:221-226).
 uint32_t next_capacity(uint32_t needed, uint32_t current, uint32_t growth, uint32_t maximum) {

@@ -151,6 +151,32 @@ struct GatherArgs {
     uint8_t* values;  // [count][kv_heads][head_dim] in the storage type
 };
 
+// One matrix of a projection in the device layout of q8_layout.h: its row tiles are blockIdx.x values
+// first_tile .. first_tile + q8_tiles(rows) - 1 of the launch.
+struct ProjectionSegment {
+    const uint8_t* codes;
+    const uint16_t* scales;  // FP16 bits
+    const float* bias;       // null: no bias
+    int32_t rows;
+    int32_t first_tile;
+    int32_t out_column;
+    int32_t pad;
+};
+
+struct ProjectionArgs {
+    ProjectionSegment segment[3];
+    int32_t segments;
+    int32_t columns;
+    int32_t chunks;  // q8_chunks(columns)
+    int32_t tokens;
+    int32_t in_stride;
+    int32_t out_stride;
+    int32_t accumulate;
+    int32_t pad;
+    const float* input;  // 16-byte aligned rows
+    float* output;
+};
+
 // Page regions are stored in MFMA-fragment order; see page_layout.h.
 
 // Where a kernel goes: the cache's stream, and (when profiling) the events its dispatch records at start and end.
@@ -178,6 +204,9 @@ int prefill_resident_blocks(int device, int head_dim, int group);
 // Prefill items [first, first + items) with `tiles` (1 or kPrefillTiles) column tiles of 16 tokens per wave.
 hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int first, int items, int tiles, bool fp16);
 hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16);
+// A projection over `tiles` row tiles (all segments); token tiles of 16 * projection_token_tiles(tokens).
+hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles);
+int projection_token_tiles(int tokens);
 
 // Query rows (tokens) per prefill work item: 16 per MFMA column tile, kPrefillTiles tiles per wave.
 constexpr int kPrefillTiles = 2;

@@ -1,0 +1,249 @@
+// Host half of the Q8_0 projections: the weights handle (upload and repack of GGML Q8_0 matrices), validation of a
+// projection against matmul_args' rules (common.metal:54-71, locate_segment :138-146) and its launch.
+//
+// The reference binds the mapped model file and passes byte offsets per matrix (GpuLayoutMapping.cs:14-32,
+// MatmulSegment params.rs); here the offsets select the matrices once, at upload, and a projection names them by
+// index.
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "abi_support.h"
+#include "kv_internal.h"
+#include "q8_layout.h"
+
+namespace synapse_kv {
+namespace {
+
+struct DeviceMatrix {
+    uint32_t rows = 0;
+    uint32_t columns = 0;
+    size_t codes = 0;   // byte offsets into the weights' device memory
+    size_t scales = 0;
+    size_t bias = 0;
+    bool has_bias = false;
+};
+
+size_t align_to(size_t value, size_t alignment) { return (value + alignment - 1) / alignment * alignment; }
+
+}  // namespace
+}  // namespace synapse_kv
+
+struct SynapseKvWeights {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint8_t* memory = nullptr;
+    size_t bytes = 0;
+    std::vector<synapse_kv::DeviceMatrix> matrices;
+    std::vector<const void*> checked_pointers;  // device addresses that passed the check, most recent first
+
+    ~SynapseKvWeights() {
+        if (memory != nullptr) {
+            (void)hipSetDevice(device);
+            (void)hipStreamSynchronize(stream);
+            (void)hipFree(memory);
+        }
+    }
+};
+
+namespace synapse_kv {
+namespace {
+
+void check_device_pointer(SynapseKvWeights& weights, const void* pointer, const char* name) {
+    if (pointer == nullptr) {
+        fail(SYNAPSE_KV_NULL_POINTER, std::string("null pointer: ") + name);
+    }
+    auto& seen = weights.checked_pointers;
+    if (std::find(seen.begin(), seen.end(), pointer) != seen.end()) {
+        return;
+    }
+    hipPointerAttribute_t attributes{};
+    if (hipPointerGetAttributes(&attributes, pointer) != hipSuccess || attributes.type != hipMemoryTypeDevice) {
+        (void)hipGetLastError();
+        invalid(std::string(name) + " must be device memory");
+    }
+    seen.insert(seen.begin(), pointer);
+    if (seen.size() > 16) {
+        seen.pop_back();
+    }
+}
+
+void create_weights(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMatrix* matrices, uint32_t count,
+                    SynapseKvWeights** out) {
+    if (count == 0) {
+        invalid("at least one matrix");
+    }
+    std::vector<DeviceMatrix> layout(count);
+    size_t total = 0;
+    for (uint32_t index = 0; index < count; ++index) {
+        const SynapseKvMatrix& m = matrices[index];
+        const std::string name = "matrix " + std::to_string(index);
+        if (m.rows == 0 || m.columns == 0 || m.columns % kQ8BlockElements != 0) {
+            invalid(name + ": rows must be positive and columns a positive multiple of 32");
+        }
+        const uint64_t weight_bytes = static_cast<uint64_t>(m.rows) * (m.columns / kQ8BlockElements) * kQ8BlockBytes;
+        if (m.weight > blob_bytes || weight_bytes > blob_bytes - m.weight) {
+            invalid(name + ": its Q8_0 rows extend past the blob");
+        }
+        if (m.bias != SYNAPSE_KV_NO_BIAS &&
+            (m.bias > blob_bytes || static_cast<uint64_t>(m.rows) * 4 > blob_bytes - m.bias || m.bias % 4 != 0)) {
+            invalid(name + ": its biases extend past the blob or are not 4-byte aligned");
+        }
+        DeviceMatrix& d = layout[index];
+        d.rows = m.rows;
+        d.columns = m.columns;
+        const size_t tiles = static_cast<size_t>(q8_tiles(static_cast<int>(m.rows))) * q8_chunks(static_cast<int>(m.columns));
+        d.codes = total;
+        total = align_to(total + tiles * kQ8TileBytes, 256);
+        d.scales = total;
+        total = align_to(total + tiles * kQ8TileScales * sizeof(uint16_t), 256);
+        d.has_bias = m.bias != SYNAPSE_KV_NO_BIAS;
+        if (d.has_bias) {
+            d.bias = total;
+            total = align_to(total + static_cast<size_t>(m.rows) * 4, 256);
+        }
+    }
+    std::vector<uint8_t> staging(total, 0);
+    for (uint32_t index = 0; index < count; ++index) {
+        const SynapseKvMatrix& m = matrices[index];
+        const DeviceMatrix& d = layout[index];
+        q8_repack(blob + m.weight, static_cast<int>(m.rows), static_cast<int>(m.columns), staging.data() + d.codes,
+                  reinterpret_cast<uint16_t*>(staging.data() + d.scales));
+        if (d.has_bias) {
+            std::memcpy(staging.data() + d.bias, blob + m.bias, static_cast<size_t>(m.rows) * 4);
+        }
+    }
+    auto* weights = new SynapseKvWeights();
+    try {
+        check_hip(hipGetDevice(&weights->device), "current device");
+        weights->bytes = total;
+        weights->matrices = std::move(layout);
+        check_hip(hipMalloc(reinterpret_cast<void**>(&weights->memory), std::max<size_t>(total, 1)), "weights");
+        check_hip(hipMemcpy(weights->memory, staging.data(), total, hipMemcpyHostToDevice), "weights upload");
+    } catch (...) {
+        delete weights;
+        throw;
+    }
+    *out = weights;
+}
+
+void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output) {
+    if (p.segments < 1 || p.segments > 3) {
+        invalid("a projection has 1..3 segments");
+    }
+    if (p.tokens == 0 || p.accumulate > 1 || p.reserved != 0) {
+        invalid("tokens must be positive, accumulate 0 or 1 and reserved 0");
+    }
+    ProjectionArgs args{};
+    int tiles = 0;
+    uint32_t columns = 0;
+    for (uint32_t s = 0; s < p.segments; ++s) {
+        if (p.matrix[s] >= weights.matrices.size()) {
+            invalid("segment " + std::to_string(s) + " names matrix " + std::to_string(p.matrix[s]) + " of " +
+                    std::to_string(weights.matrices.size()));
+        }
+        const DeviceMatrix& m = weights.matrices[p.matrix[s]];
+        if (s == 0) {
+            columns = m.columns;
+        } else if (m.columns != columns) {
+            invalid("the segments' matrices must have equal column counts");
+        }
+        if (static_cast<uint64_t>(p.out_column[s]) + m.rows > p.out_stride) {
+            invalid("segment " + std::to_string(s) + " writes past out_stride");
+        }
+        ProjectionSegment& seg = args.segment[s];
+        seg.codes = weights.memory + m.codes;
+        seg.scales = reinterpret_cast<const uint16_t*>(weights.memory + m.scales);
+        seg.bias = m.has_bias ? reinterpret_cast<const float*>(weights.memory + m.bias) : nullptr;
+        seg.rows = static_cast<int32_t>(m.rows);
+        seg.first_tile = tiles;
+        seg.out_column = static_cast<int32_t>(p.out_column[s]);
+        tiles += q8_tiles(static_cast<int>(m.rows));
+    }
+    if (p.in_stride < columns || p.in_stride % 4 != 0) {
+        invalid("in_stride must be a multiple of 4 and hold the " + std::to_string(columns) + " input columns");
+    }
+    if (reinterpret_cast<uintptr_t>(input) % 16 != 0) {
+        invalid("input must be 16-byte aligned");
+    }
+    check_hip(hipSetDevice(weights.device), "set device");
+    check_device_pointer(weights, input, "input");
+    check_device_pointer(weights, output, "output");
+    args.segments = static_cast<int32_t>(p.segments);
+    args.columns = static_cast<int32_t>(columns);
+    args.chunks = q8_chunks(static_cast<int>(columns));
+    args.tokens = static_cast<int32_t>(p.tokens);
+    args.in_stride = static_cast<int32_t>(p.in_stride);
+    args.out_stride = static_cast<int32_t>(p.out_stride);
+    args.accumulate = static_cast<int32_t>(p.accumulate);
+    args.input = input;
+    args.output = output;
+    check_hip(launch_projection(Launch{weights.stream, nullptr, nullptr}, args, tiles), "projection");
+}
+
+}  // namespace
+}  // namespace synapse_kv
+
+using namespace synapse_kv;
+
+extern "C" {
+
+int32_t synapse_kv_weights_create(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMatrix* matrices,
+                                  uint32_t count, SynapseKvWeights** weights) {
+    if (blob == nullptr || matrices == nullptr || weights == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: blob, matrices or output");
+    }
+    return guarded([&] { create_weights(blob, blob_bytes, matrices, count, weights); });
+}
+
+void synapse_kv_weights_destroy(SynapseKvWeights* weights) { delete weights; }
+
+uint64_t synapse_kv_weights_bytes(const SynapseKvWeights* weights) { return weights == nullptr ? 0 : weights->bytes; }
+
+int32_t synapse_kv_weights_set_stream(SynapseKvWeights* weights, void* stream) {
+    if (weights == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: weights");
+    }
+    return guarded([&] {
+        check_hip(hipSetDevice(weights->device), "set device");
+        check_hip(hipStreamSynchronize(weights->stream), "stream switch");
+        weights->stream = static_cast<hipStream_t>(stream);
+    });
+}
+
+int32_t synapse_kv_project(SynapseKvWeights* weights, const SynapseKvProjection* projection, const float* input,
+                           float* output) {
+    if (weights == nullptr || projection == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: weights or projection");
+    }
+    return guarded([&] { project(*weights, *projection, input, output); });
+}
+
+int32_t synapse_kv_weights_read(SynapseKvWeights* weights, uint32_t index, uint8_t* blocks, uint64_t bytes) {
+    if (weights == nullptr || blocks == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: weights or blocks");
+    }
+    return guarded([&] {
+        if (index >= weights->matrices.size()) {
+            invalid("matrix " + std::to_string(index) + " of " + std::to_string(weights->matrices.size()));
+        }
+        const DeviceMatrix& m = weights->matrices[index];
+        const uint64_t needed = static_cast<uint64_t>(m.rows) * (m.columns / kQ8BlockElements) * kQ8BlockBytes;
+        if (bytes < needed) {
+            invalid("the matrix needs " + std::to_string(needed) + " bytes");
+        }
+        const size_t tiles = static_cast<size_t>(q8_tiles(static_cast<int>(m.rows))) * q8_chunks(static_cast<int>(m.columns));
+        std::vector<uint8_t> codes(tiles * kQ8TileBytes);
+        std::vector<uint16_t> scales(tiles * kQ8TileScales);
+        check_hip(hipSetDevice(weights->device), "set device");
+        check_hip(hipStreamSynchronize(weights->stream), "weights read");
+        check_hip(hipMemcpy(codes.data(), weights->memory + m.codes, codes.size(), hipMemcpyDeviceToHost), "weights read");
+        check_hip(hipMemcpy(scales.data(), weights->memory + m.scales, scales.size() * 2, hipMemcpyDeviceToHost),
+                  "weights read");
+        q8_unpack(codes.data(), scales.data(), static_cast<int>(m.rows), static_cast<int>(m.columns), blocks);
+    });
+}
+
+}  // extern "C"

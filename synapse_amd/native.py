@@ -16,7 +16,7 @@ import ctypes
 import threading
 from pathlib import Path
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libsynapse_kv.so"
 
 STATUS_OK = 0
@@ -113,13 +113,42 @@ class PageStats(ctypes.Structure):
 
 KERNEL_KINDS = ("table", "pages", "append", "decode", "merge", "prefill", "gather")
 
+NO_BIAS = (1 << 64) - 1
+
+
+class Matrix(ctypes.Structure):
+    """SynapseKvMatrix: one GGML Q8_0 matrix of a host blob (matmul_segment's weight/bias/rows)."""
+
+    _fields_ = [
+        ("weight", ctypes.c_uint64),
+        ("bias", ctypes.c_uint64),
+        ("rows", ctypes.c_uint32),
+        ("columns", ctypes.c_uint32),
+    ]
+
+
+class Projection(ctypes.Structure):
+    """SynapseKvProjection: matmul_args (common.metal:61-71) with matrices named by index."""
+
+    _fields_ = [
+        ("matrix", ctypes.c_uint32 * 3),
+        ("out_column", ctypes.c_uint32 * 3),
+        ("segments", ctypes.c_uint32),
+        ("tokens", ctypes.c_uint32),
+        ("in_stride", ctypes.c_uint32),
+        ("out_stride", ctypes.c_uint32),
+        ("accumulate", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
 
 class Profile(ctypes.Structure):
     _fields_ = [("launches", ctypes.c_uint64 * 8), ("milliseconds", ctypes.c_double * 8)]
 
 
 # Sizes pinned on both sides of the ABI (include/synapse_kv.h static assertions).
-STRUCT_SIZES = {DeviceInfo: 152, BatchToken: 16, CacheDesc: 64, PageStats: 40, Profile: 128}
+STRUCT_SIZES = {DeviceInfo: 152, BatchToken: 16, CacheDesc: 64, PageStats: 40, Profile: 128, Matrix: 24,
+                Projection: 48}
 for _struct, _size in STRUCT_SIZES.items():
     assert ctypes.sizeof(_struct) == _size, (_struct.__name__, ctypes.sizeof(_struct))
 
@@ -160,6 +189,12 @@ EXPORTS = {
     "synapse_kv_page_stats": (_I32, [_P, ctypes.POINTER(PageStats)]),
     "synapse_kv_read_kv": (_I32, [_P, _U32, _U32, _U32, _U32, _P, _P]),
     "synapse_kv_rope_table": (_I32, [_U32, ctypes.c_float, ctypes.c_float, _U32, _U32, _P, _P]),
+    "synapse_kv_weights_create": (_I32, [_P, _U64, ctypes.POINTER(Matrix), _U32, ctypes.POINTER(_P)]),
+    "synapse_kv_weights_destroy": (None, [_P]),
+    "synapse_kv_weights_bytes": (_U64, [_P]),
+    "synapse_kv_weights_set_stream": (_I32, [_P, _P]),
+    "synapse_kv_project": (_I32, [_P, ctypes.POINTER(Projection), _P, _P]),
+    "synapse_kv_weights_read": (_I32, [_P, _U32, _P, _U64]),
 }
 
 

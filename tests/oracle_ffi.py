@@ -54,6 +54,8 @@ SIGNATURES = {
     "orc_prefix_claim": (_I, [_P, _P, _I]),
     "orc_prefix_remember": (None, [_P, _P, _I, _P, _I]),
     "orc_prefix_clear": (None, [_P]),
+    "orc_q8_project_f32": (ctypes.c_double, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P, _I, _I, _I]),
+    "orc_q8_project_f64": (None, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P, _I, _I, _P]),
 }
 
 
@@ -274,3 +276,28 @@ class Prefix:
 
     def clear(self):
         ORACLE.orc_prefix_clear(self.handle)
+
+
+def q8_project(segments, inputs, output, accumulate=False, exact=False, threads=1):
+    """A Q8_0 projection on the restatement. ``segments``: [(blocks uint8 [rows][columns / 32 * 34], bias float32
+    [rows] or None, out_column)]; ``inputs`` float32 [tokens][>= columns]; ``output`` float32 [tokens][stride],
+    updated in place. ``exact``: the FP64 anchor, returning sum |terms| per element; otherwise the reference's FP32
+    matrix-vector order, returning the wall time in seconds."""
+    count = len(segments)
+    blocks = [np.ascontiguousarray(b, dtype=np.uint8) for b, _, _ in segments]
+    biases = [None if bias is None else np.ascontiguousarray(bias, dtype=np.float32) for _, bias, _ in segments]
+    weights = (ctypes.c_void_p * count)(*[b.ctypes.data for b in blocks])
+    bias_pointers = (ctypes.c_void_p * count)(*[None if b is None else b.ctypes.data for b in biases])
+    rows = (ctypes.c_int * count)(*[b.shape[0] for b in blocks])
+    columns = blocks[0].shape[1] // 34 * 32
+    out_columns = (ctypes.c_int * count)(*[int(column) for _, _, column in segments])
+    inputs = np.ascontiguousarray(inputs, dtype=np.float32)
+    assert output.dtype == np.float32 and output.flags["C_CONTIGUOUS"]
+    tokens = inputs.shape[0]
+    if exact:
+        magnitude = np.zeros(output.shape, dtype=np.float64)
+        ORACLE.orc_q8_project_f64(weights, bias_pointers, rows, out_columns, count, columns, tokens, ptr(inputs),
+                                  inputs.shape[1], ptr(output), output.shape[1], int(accumulate), ptr(magnitude))
+        return magnitude
+    return ORACLE.orc_q8_project_f32(weights, bias_pointers, rows, out_columns, count, columns, tokens, ptr(inputs),
+                                     inputs.shape[1], ptr(output), output.shape[1], int(accumulate), threads)

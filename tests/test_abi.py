@@ -41,7 +41,7 @@ def test_header_compiles_with_pinned_sizes(compiler, flag, tmp_path):
 def test_abi_version_and_struct_sizes(native):
     from synapse_amd.native import ABI_VERSION, STRUCT_SIZES
 
-    assert native.c_abi_version() == ABI_VERSION == 1
+    assert native.c_abi_version() == ABI_VERSION == 2
     for struct, size in STRUCT_SIZES.items():
         assert ctypes.sizeof(struct) == size
 
@@ -69,6 +69,12 @@ def test_null_pointers_and_last_error_protocol(native):
     assert native.c_attention(None, 0, None, 0, None, 0) == 1
     assert native.c_bytes(None) == 0
     native.c_cache_destroy(None)  # null is ignored
+    assert native.c_weights_create(None, 0, None, 0, None) == 1
+    assert native.c_project(None, None, None, None) == 1
+    assert native.c_weights_set_stream(None, None) == 1
+    assert native.c_weights_read(None, 0, None, 0) == 1
+    assert native.c_weights_bytes(None) == 0
+    native.c_weights_destroy(None)  # null is ignored
 
 
 def test_status_maps_to_the_managed_exceptions(native):
@@ -113,3 +119,23 @@ def test_rope_table_entry_point_matches_the_restatement(native):
         assert np.array_equal(sin.view(np.uint32), osin.view(np.uint32))
     out = np.zeros(4, dtype=np.float32)
     assert native.c_rope_table(63, 1e6, 0.0, 0, 1, out.ctypes.data, out.ctypes.data) == 2
+
+
+@pytest.mark.parametrize("rows,columns,weight,bias,count", [
+    (4, 48, 0, None, 1),        # columns not a multiple of 32
+    (0, 64, 0, None, 1),        # no rows
+    (4, 64, 40, None, 1),       # rows run past the blob (4 * 2 * 34 = 272 bytes from offset 40 of 300)
+    (4, 64, 0, 298, 1),         # biases run past the blob
+    (4, 64, 0, 2, 1),           # biases not 4-byte aligned
+    (4, 64, 0, None, 0),        # no matrices
+])
+def test_weights_create_validates_before_the_device(native, rows, columns, weight, bias, count):
+    from synapse_amd.native import NO_BIAS, Matrix
+
+    blob = np.zeros(300, dtype=np.uint8)
+    matrix = Matrix(weight, NO_BIAS if bias is None else bias, rows, columns)
+    handle = ctypes.c_void_p()
+    assert native.c_weights_create(blob.ctypes.data, blob.nbytes, ctypes.byref(matrix), count,
+                                   ctypes.byref(handle)) == 2
+    assert "invalid argument" in native.last_error()
+    assert not handle.value
