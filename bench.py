@@ -407,12 +407,148 @@ def config_c4(args, torch) -> dict:
     return line
 
 
+def projection_blob(rng, shapes, bias_flags):
+    """One layer's Q8_0 matrices as GGML blocks (random codes, FP16 scales around 1/64) with FP32 biases."""
+    parts, matrices, offset = [], [], 0
+    for (rows, columns), with_bias in zip(shapes, bias_flags):
+        blocks = np.empty((rows, columns // 32, 34), dtype=np.uint8)
+        blocks[:, :, 2:] = rng.integers(-127, 128, size=(rows, columns // 32, 32), dtype=np.int8).view(np.uint8)
+        scales = (rng.random((rows, columns // 32), dtype=np.float32) * np.float32(1 / 32)).astype(np.float16)
+        blocks[:, :, :2] = scales.view(np.uint8).reshape(rows, columns // 32, 2)
+        entry = {"weight": offset, "rows": rows, "columns": columns}
+        parts.append(blocks.reshape(-1))
+        offset += blocks.nbytes
+        if with_bias:
+            bias = rng.standard_normal(rows).astype(np.float32)
+            entry["bias"] = offset
+            parts.append(bias.view(np.uint8))
+            offset += bias.nbytes
+        matrices.append(entry)
+    return np.concatenate(parts), matrices
+
+
+def config_projection(args, torch) -> dict:
+    """Q8_0 projections around the attention path on the 7B shape (hidden 3,584; QKV 4,608 rows with biases; o_proj
+    3,584 rows accumulating into the residual), 28 layers of distinct weights. The headline is the decode step of
+    C3 (16 tokens): weight bytes streamed per second against HBM. The prompt projection of C5 (2,048 tokens) is
+    reported beside it in TFLOP/s against the FP32 MFMA peak (the reference's FP32 numeric contract)."""
+    from synapse_amd.projection import Q8Weights
+
+    hidden, kv = HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM
+    shapes = [(hidden, hidden), (kv, hidden), (kv, hidden), (hidden, hidden)]
+    rng = np.random.default_rng(SEED + 7)
+    layer_blob, layer_matrices = projection_blob(rng, shapes, [True, True, True, False])
+    blob = np.tile(layer_blob, LAYERS)
+    matrices = [dict(m, weight=m["weight"] + layer * layer_blob.nbytes,
+                     **({"bias": m["bias"] + layer * layer_blob.nbytes} if "bias" in m else {}))
+                for layer in range(LAYERS) for m in layer_matrices]
+    weights = Q8Weights(blob, matrices)
+    stream = torch.cuda.current_stream()
+    weights.set_stream(stream)
+    log(f"projection weights {weights.device_bytes / 2**20:.1f} MiB on the device")
+    qkv_rows = hidden + 2 * kv
+    element_bytes = 34 / 32  # codes plus FP16 scales per weight element, as in the GGML blocks
+
+    def measure(tokens: int, repetitions: int):
+        x = torch.randn((tokens, hidden), device="cuda")
+        qkv = torch.empty((tokens, qkv_rows), device="cuda")
+        attention = torch.randn((tokens, hidden), device="cuda")
+        residual = torch.randn((tokens, hidden), device="cuda")
+
+        def layer_pair(layer):
+            base = 4 * layer
+            weights.project([(base, 0), (base + 1, hidden), (base + 2, hidden + kv)], x, qkv)
+            weights.project([(base + 3, 0)], attention, residual, accumulate=True)
+
+        def qkv_only(layer):
+            base = 4 * layer
+            weights.project([(base, 0), (base + 1, hidden), (base + 2, hidden + kv)], x, qkv)
+
+        def o_only(layer):
+            weights.project([(4 * layer + 3, 0)], attention, residual, accumulate=True)
+
+        results = {}
+        for name, body in (("step", layer_pair), ("qkv", qkv_only), ("o_proj", o_only)):
+            for _ in range(args.warmup):
+                for layer in range(LAYERS):
+                    body(layer)
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record(stream)
+            for _ in range(repetitions):
+                for layer in range(LAYERS):
+                    body(layer)
+            stop.record(stream)
+            torch.cuda.synchronize()
+            results[name] = start.elapsed_time(stop) * 1e-3 / repetitions  # seconds per 28 layers
+        return results
+
+    decode_tokens, prompt_tokens = SEQUENCES, 2048
+    decode = measure(decode_tokens, args.steps)
+    prompt = measure(prompt_tokens, max(1, args.steps // 10))
+    qkv_weight = qkv_rows * hidden * element_bytes
+    o_weight = hidden * hidden * element_bytes
+    qkv_bytes = qkv_weight + decode_tokens * (hidden + qkv_rows) * 4
+    o_bytes = o_weight + decode_tokens * hidden * 4 * 3  # input, residual read and write
+    step_bytes = LAYERS * (qkv_bytes + o_bytes)
+    qkv_us = decode["qkv"] / LAYERS * 1e6
+    qkv_gbps = qkv_bytes / (qkv_us * 1e-6) / 1e9
+    flops = 2 * prompt_tokens * (qkv_rows + hidden) * hidden
+    prompt_tflops = LAYERS * flops / prompt["step"] / 1e12
+    qkv_flops = 2 * prompt_tokens * qkv_rows * hidden
+    prompt_qkv_tflops = LAYERS * qkv_flops / prompt["qkv"] / 1e12
+    line = {
+        "metric": "Q8_0 projection (QKV + o_proj) weight-stream GB/s, 7B shape, 16 decode tokens",
+        "value": round(step_bytes / decode["step"] / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(decode["step"] * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q8_0 x f32 (f32 accumulate)",
+        "data": f"synthetic Q8_0 weights (numpy seed {SEED + 7}), 28 distinct layers; torch N(0,1) activations",
+        "config": {"workload": "7B projections: QKV 4,608 x 3,584 with biases + o_proj 3,584 x 3,584 accumulating, "
+                               "28 layers, 16 tokens", "decode_tokens": decode_tokens, "prompt_tokens": prompt_tokens},
+        "roofline": {"bound": "hbm", "kernel": "project_kernel<1> (QKV, 3 segments)", "achieved": round(qkv_gbps, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(qkv_gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": int(qkv_bytes),
+                     "avg_launch_us": round(qkv_us, 2),
+                     "o_proj_avg_launch_us": round(decode["o_proj"] / LAYERS * 1e6, 2)},
+        "prompt": {"tokens": prompt_tokens, "ms_per_28_layers": round(prompt["step"] * 1e3, 3),
+                   "tflops": round(prompt_tflops, 1), "qkv_tflops": round(prompt_qkv_tflops, 1),
+                   "peak_fp32_mfma_tflops": 157.3, "frac": round(prompt_tflops / 157.3, 4)},
+    }
+    weights.close()
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, str(ROOT / "tests"))
+        from oracle_ffi import q8_project
+
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        layer = layer_blob
+        segments = []
+        for index, m in enumerate(layer_matrices[:3]):
+            rows, columns = m["rows"], m["columns"]
+            blocks = layer[m["weight"]:m["weight"] + rows * columns // 32 * 34].reshape(rows, -1)
+            bias = layer[m["bias"]:m["bias"] + rows * 4].view(np.float32) if "bias" in m else None
+            segments.append((blocks, bias, [0, hidden, hidden + kv][index]))
+        o = layer_matrices[3]
+        o_blocks = layer[o["weight"]:o["weight"] + hidden * hidden // 32 * 34].reshape(hidden, -1)
+        x = rng.standard_normal((decode_tokens, hidden), dtype=np.float32)
+        out = np.zeros((decode_tokens, qkv_rows), dtype=np.float32)
+        residual = np.zeros((decode_tokens, hidden), dtype=np.float32)
+        seconds = q8_project(segments, x, out, threads=threads)
+        seconds += q8_project([(o_blocks, None, 0)], x, residual, accumulate=True, threads=threads)
+        line["cpu_baseline"] = {
+            "value": round(LAYERS * (qkv_bytes + o_bytes) / 1e9 / (LAYERS * seconds), 2), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"one layer's QKV + o_proj for 16 tokens ({seconds * 1e3:.0f} ms) in the reference's FP32 "
+                      f"matrix-vector order (matmul.cu q8_matvec restated in C++), {threads} std::threads, x28 layers",
+        }
+    return line
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5"], default="c3",
+    parser.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5", "proj"], default="c3",
                         help="c3: the BASELINE metric (default); c1, c2, c4: the other decode configurations; "
-                             "c5: chunked-prefill MFMA throughput")
+                             "c5: chunked-prefill MFMA throughput; proj: the Q8_0 projections around the path")
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--split-keys", type=int, default=None)
@@ -437,7 +573,8 @@ def main() -> None:
         sys.exit("bench.py needs a HIP device")
     torch.cuda.set_device(0)
     if args.config != "c3":
-        runner = {"c1": config_c1, "c2": config_c2, "c4": config_c4, "c5": prefill_config}[args.config]
+        runner = {"c1": config_c1, "c2": config_c2, "c4": config_c4, "c5": prefill_config,
+                  "proj": config_projection}[args.config]
         print(json.dumps(runner(args, torch)), flush=True)
         return
     lengths = lengths_for(SEED + CONFIG_OFFSET)

@@ -172,9 +172,14 @@ struct ProjectionArgs {
     int32_t in_stride;
     int32_t out_stride;
     int32_t accumulate;
-    int32_t pad;
-    const float* input;  // 16-byte aligned rows
+    int32_t padded_columns;  // chunks * 64
+    const float* input;      // 16-byte aligned rows
     float* output;
+    __bf16* parts;           // the exact 3-part bf16 split of the input in MFMA fragment order (scratch)
+    int32_t total_tiles;     // row tiles over all segments
+    int32_t slices;          // decode: column slices (projection_decode_slices)
+    float* partials;         // decode: [slices][16][partial_stride] per-slice sums (scratch)
+    int64_t partial_stride;  // total_tiles * 16
 };
 
 // Page regions are stored in MFMA-fragment order; see page_layout.h.
@@ -207,6 +212,8 @@ hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16
 // A projection over `tiles` row tiles (all segments); token tiles of 16 * projection_token_tiles(tokens).
 hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles);
 int projection_token_tiles(int tokens);
+// Column slices of a decode projection (tokens <= 16) over `chunks` 64-column chunks.
+int projection_decode_slices(int chunks);
 
 // Query rows (tokens) per prefill work item: 16 per MFMA column tile, kPrefillTiles tiles per wave.
 constexpr int kPrefillTiles = 2;

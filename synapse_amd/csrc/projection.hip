@@ -1,21 +1,29 @@
-// Q8_0 projections (QKV before the attention path, o_proj after it) on FP32 MFMA.
+// Q8_0 projections (QKV before the attention path, o_proj after it) on bf16 MFMA with exact products.
 //
 // Semantics: synapse_q8_matvec_{1,2,4,8} and synapse_q8_gemm (native/synapse-gpu/src/Features/GpuKernels/cuda/
 // kernels/matmul.cu:1-189, metal/shaders/matmul.metal:1-310): output[t][out_column + row] = (accumulate ? output : 0)
-// + sum_k (d * code)[row][k] * input[t][k] + bias[row], rows of up to three matrices in one dispatch
-// (locate_segment, common.metal:138-146). Weights stay Q8_0, activations stay FP32 and every product and sum is
-// FP32 (ADR-012): the weight element d * code is exact in FP32 (an 11-bit by 8-bit product) and the MFMA multiplies
-// and accumulates in FP32, so only the summation order differs from the reference's kernels.
+// + sum_blocks d * sum_k code[row][k] * input[t][k] + bias[row], rows of up to three matrices in one dispatch
+// (locate_segment, common.metal:138-146). Weights stay Q8_0, activations FP32, sums FP32 (ADR-012).
 //
-// MI355X mapping: one workgroup of four waves per (16-row tile, 16 * NT tokens). The waves split the columns into
-// four contiguous ranges of 64-column chunks; per chunk a wave loads its tile's 1 KiB of codes (one 16-byte load per
-// lane, fragment order, see q8_layout.h), the 16 rows' scales and, per token tile, 16 consecutive input values per
-// lane, then runs 16 v_mfma_f32_16x16x4_f32 per token tile (lane g of the MFMA's k dimension takes columns
-// 16 g + j of the chunk in MFMA j, for both operands). The next chunk's loads are in flight while the current one
-// computes. The four waves' 16 x 16 * NT sums meet in LDS and are added in wave order.
+// Exact products on the bf16 matrix cores: each FP32 input x is split into three bf16 parts with
+// x = hi + mid + lo exactly (bf16 keeps FP32's exponent range; each part takes the next 8 significant bits, and the
+// residuals x - hi and (x - hi) - mid are exact FP32 subtractions). A Q8_0 code is exact in bf16, and code * part
+// is a product of at most 8 by 8 significant bits, exact in FP32. One Q8_0 block (32 columns) is one k-depth of
+// v_mfma_f32_16x16x32_bf16: the block's three MFMAs (lo, mid, hi parts) sum its exact products in FP32 into a fresh
+// accumulator, and the block's sum is then scaled and added as the reference does (sum = fma(block dot, d, sum),
+// matmul.cu:101-104). Only the order of the FP32 additions differs from the reference's kernels.
+//
+// MI355X mapping: split_kernel writes the three parts of the input once per projection, in the B-operand fragment
+// order of the MFMA (zero past the matrix's columns and the last token). project_kernel: one workgroup per
+// (16-row tile, 16 * NT tokens);
+// the waves split the columns into contiguous ranges of 64-column chunks (two blocks). Per chunk a wave loads
+// its tile's 1 KiB of codes (one 16-byte load per lane, fragment order, see q8_layout.h), the scales of its
+// accumulator rows, and per token tile the six 16-byte B fragments (part x block); chunks are loaded in groups
+// ahead of the multiplies. The waves' 16 x 16 * NT sums meet in LDS and are added in wave order, then the bias
+// and the residual.
 //
 // The same kernel serves decode (NT = 1: up to 16 tokens, the weight stream dominates) and prompt runs (NT = 4:
-// 64 tokens per workgroup, each weight tile reused from registers for four token tiles).
+// 64 tokens per workgroup, each weight tile converted once and used for four token tiles).
 
 #include "kv_internal.h"
 #include "q8_layout.h"
@@ -25,56 +33,148 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t uintx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uintx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kProjectionWaves = 4;
-
+// Waves per workgroup (each takes an equal contiguous range of the column chunks): eight for decode, so a SIMD
+// holds about two waves of a layer-sized launch and one wave's loads hide behind another's multiplies; four for
+// prompt runs, whose workgroups already fill the device.
 template <int NT>
-struct ChunkOperands {
-    uintx4 codes;        // 16 codes of row r, columns 16 g .. + 15 of the chunk
-    float scale;         // d of row r for the block holding those columns
-    floatx4 x[NT][4];    // per token tile: input[token 16 c + r][16 g .. + 15 of the chunk]
+constexpr int projection_waves() {
+    return NT == 1 ? 8 : 4;
+}
+constexpr int kParts = 3;
+
+// x = hi + mid + lo, each part rounded to nearest bf16; the residuals are exact in FP32 and lo holds the last (at
+// most 8) significant bits exactly.
+__device__ inline void split3(float x, __bf16& hi, __bf16& mid, __bf16& lo) {
+#pragma clang fp contract(off)
+    hi = static_cast<__bf16>(x);
+    const float first = x - static_cast<float>(hi);
+    mid = static_cast<__bf16>(first);
+    lo = static_cast<__bf16>(first - static_cast<float>(mid));
+}
+
+// Element offset of the parts of (token, column) in the split input: [token tile][chunk][part][block][lane][8],
+// lane = 16 g + t holding columns 8 g .. 8 g + 7 of the block for token 16 tile + t, so every B-fragment load of
+// the projection kernel is one contiguous 1 KiB wave load. The tile's three parts follow each other per chunk.
+__device__ inline size_t part_offset(int chunks, int token, int column, int part) {
+    const int tile = token / 16;
+    const int t = token % 16;
+    const int chunk = column / kQ8ChunkColumns;
+    const int block = (column % kQ8ChunkColumns) / kQ8BlockElements;
+    const int g = (column % kQ8BlockElements) / 8;
+    return ((((static_cast<size_t>(tile) * chunks + chunk) * kParts + part) * 2 + block) * 64 + 16 * g + t) * 8 +
+           column % 8;
+}
+
+// One thread per (token, 8 columns): the three bf16 parts of input[token][8 j .. 8 j + 7] (zeros past `columns`),
+// stored in fragment order.
+__global__ __launch_bounds__(256) void split_kernel(ProjectionArgs a) {
+    const int groups = a.padded_columns / 8;
+    const int index = blockIdx.x * 256 + threadIdx.x;
+    if (index >= a.tokens * groups) {
+        return;
+    }
+    const int token = index / groups;
+    const int column = (index % groups) * 8;
+    float values[8];
+    if (column < a.columns) {
+        const floatx4* source = reinterpret_cast<const floatx4*>(a.input + static_cast<size_t>(token) * a.in_stride + column);
+        const floatx4 first = source[0];
+        const floatx4 second = source[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            values[i] = first[i];
+            values[i + 4] = second[i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            values[i] = 0.0f;
+        }
+    }
+    bf16x8 parts[kParts];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        __bf16 hi;
+        __bf16 mid;
+        __bf16 lo;
+        split3(values[i], hi, mid, lo);
+        parts[0][i] = hi;
+        parts[1][i] = mid;
+        parts[2][i] = lo;
+    }
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) {
+        *reinterpret_cast<bf16x8*>(a.parts + part_offset(a.chunks, token, column, p)) = parts[p];
+    }
+}
+
+// Per token tile and block, the three parts of columns 8 g .. 8 g + 7 of token 16 c + r (B fragments).
+template <int NT>
+struct InputFragments {
+    bf16x8 x[NT][2][kParts];
 };
 
+// Chunks per batch: a batch's loads are all issued (in the order the multiplies use them: each chunk's input
+// fragments, then its codes and scales) before its first multiply. Vector memory loads complete in issue order, so
+// a batch is one round trip; a second wave on the SIMD overlaps its own round trip with this wave's multiplies.
 template <int NT>
-__device__ inline void load_chunk(const ProjectionArgs& a, const uintx4* codes, const uint16_t* scales,
-                                  const float* const (&rows)[NT], const bool (&valid)[NT], int chunk, int g,
-                                  ChunkOperands<NT>& operands) {
-    operands.codes = __builtin_nontemporal_load(codes + static_cast<size_t>(chunk) * 64);
-    operands.scale = static_cast<float>(__builtin_bit_cast(_Float16, scales[static_cast<size_t>(chunk) * kQ8TileScales]));
-    const int column = chunk * kQ8ChunkColumns + 16 * g;
-    const bool inside = column < a.columns;  // columns are a multiple of 32: a 16-column group is all in or all out
-#pragma unroll
-    for (int c = 0; c < NT; ++c) {
-        const floatx4* source = reinterpret_cast<const floatx4*>(rows[c] + column);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            operands.x[c][q] = valid[c] && inside ? source[q] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    }
+constexpr int projection_batch() {
+    return NT == 1 ? 7 : 2;
 }
 
+// One chunk (two blocks): each block's three part products go to their own fresh accumulator, issued part by part
+// across blocks and token tiles so a dependent MFMA is 2 NT MFMAs behind the one it needs, and the block sums are
+// scaled into the running sums after all of them were issued.
 template <int NT>
-__device__ inline void multiply_chunk(const ChunkOperands<NT>& operands, floatx4 (&acc)[NT]) {
-    float weight[16];
+__device__ inline void multiply_chunk(uintx4 codes, uintx4 scales, const InputFragments<NT>& input, floatx4 (&acc)[NT]) {
+    bf16x8 weight[2];
+    float d[2][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int b = 0; b < 2; ++b) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int code = static_cast<int>(static_cast<int8_t>((operands.codes[q] >> (8 * b)) & 0xFF));
-            weight[4 * q + b] = static_cast<float>(code) * operands.scale;  // exact: |code| <= 128, d is FP16
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t word = codes[2 * b + w];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                weight[b][4 * w + i] = static_cast<__bf16>(static_cast<float>(static_cast<int8_t>((word >> (8 * i)) & 0xFF)));
+            }
+            const uint32_t pair = scales[2 * b + w];
+            d[b][2 * w] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair & 0xFFFF)));
+            d[b][2 * w + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> 16)));
+        }
+    }
+    floatx4 block[2][NT];
+#pragma unroll
+    for (int p = kParts - 1; p >= 0; --p) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+                block[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    weight[b], input.x[c][b][p], p == kParts - 1 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : block[b][c], 0,
+                    0, 0);
+            }
         }
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int b = 0; b < 2; ++b) {
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
-            acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(weight[j], operands.x[c][j / 4][j % 4], acc[c], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[c][i] = __builtin_fmaf(block[b][c][i], d[b][i], acc[c][i]);
+            }
         }
     }
 }
 
 template <int NT>
-__global__ __launch_bounds__(kProjectionWaves * 64) void project_kernel(ProjectionArgs a) {
+__global__ __launch_bounds__(projection_waves<NT>() * 64) void project_kernel(ProjectionArgs a) {
+    constexpr int kWaves = projection_waves<NT>();
+    constexpr int kBatch = projection_batch<NT>();
     int tile = blockIdx.x;
     int s = 0;
     while (s + 1 < a.segments && tile >= a.segment[s + 1].first_tile) {
@@ -82,24 +182,25 @@ __global__ __launch_bounds__(kProjectionWaves * 64) void project_kernel(Projecti
     }
     const ProjectionSegment seg = a.segment[s];
     tile -= seg.first_tile;
-    const int wave = threadIdx.x >> 6;
+    // Uniform per wave, so the chunk loop and its range tests are scalar branches.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;
-    const int r = lane & 15;
     const int token0 = blockIdx.y * 16 * NT;
     const int chunks = a.chunks;
-    const int begin = wave * chunks / kProjectionWaves;
-    const int end = (wave + 1) * chunks / kProjectionWaves;
+    const int begin = wave * chunks / kWaves;
+    const int end = (wave + 1) * chunks / kWaves;
 
     const uintx4* codes = reinterpret_cast<const uintx4*>(seg.codes + static_cast<size_t>(tile) * chunks * kQ8TileBytes) + lane;
-    const uint16_t* scales = seg.scales + static_cast<size_t>(tile) * chunks * kQ8TileScales + (g >> 1) * kQ8TileRows + r;
-    const float* rows[NT];
-    bool valid[NT];
+    // A chunk's 32 scales are 64 bytes: four 16-byte groups, one per row group g.
+    const uintx4* scales = reinterpret_cast<const uintx4*>(seg.scales + static_cast<size_t>(tile) * chunks * kQ8TileScales) + g;
+    // The split input's token tiles of this workgroup (a tile past the last token re-reads tile 0; never written).
+    const bf16x8* tiles[NT];
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
-        const int token = token0 + 16 * c + r;
-        valid[c] = token < a.tokens;
-        rows[c] = a.input + static_cast<size_t>(valid[c] ? token : 0) * a.in_stride;
+        const int tile_index = blockIdx.y * NT + c;
+        tiles[c] = reinterpret_cast<const bf16x8*>(a.parts) +
+                   static_cast<size_t>(16 * tile_index < a.tokens ? tile_index : 0) * chunks * (kParts * 2 * 64) + lane;
     }
 
     floatx4 acc[NT];
@@ -107,33 +208,50 @@ __global__ __launch_bounds__(kProjectionWaves * 64) void project_kernel(Projecti
     for (int c = 0; c < NT; ++c) {
         acc[c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    if (begin < end) {
-        // Two operand sets: the next chunk's loads are in flight while the current chunk multiplies.
-        ChunkOperands<NT> even;
-        ChunkOperands<NT> odd;
-        load_chunk<NT>(a, codes, scales, rows, valid, begin, g, even);
-        for (int chunk = begin; chunk < end; chunk += 2) {
-            if (chunk + 1 < end) {
-                load_chunk<NT>(a, codes, scales, rows, valid, chunk + 1, g, odd);
+    // A batch's loads are issued whether or not each chunk is in range (past the range they re-read the last chunk):
+    // a load under a branch would leave the wait count at the join unknown. The scheduling barrier keeps them ahead
+    // of the multiplies.
+    for (int first = begin; first < end; first += kBatch) {
+        InputFragments<NT> input[kBatch];
+        uintx4 batch_codes[kBatch];
+        uintx4 batch_scales[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int chunk = min(first + i, end - 1);
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+                const bf16x8* fragments = tiles[c] + static_cast<size_t>(chunk) * (kParts * 2 * 64);
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                    for (int p = 0; p < kParts; ++p) {
+                        input[i].x[c][b][p] = fragments[(p * 2 + b) * 64];
+                    }
+                }
             }
-            multiply_chunk<NT>(even, acc);
-            if (chunk + 1 >= end) {
-                break;
+            batch_codes[i] = __builtin_nontemporal_load(codes + static_cast<size_t>(chunk) * 64);
+            batch_scales[i] = scales[static_cast<size_t>(chunk) * 4];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            if (first + i < end) {
+                multiply_chunk<NT>(batch_codes[i], batch_scales[i], input[i], acc);
             }
-            if (chunk + 2 < end) {
-                load_chunk<NT>(a, codes, scales, rows, valid, chunk + 2, g, even);
-            }
-            multiply_chunk<NT>(odd, acc);
         }
     }
 
-    // Lane (g, t) of token tile c holds rows 4 g .. + 3 of token 16 c + t; the waves' column ranges meet here.
-    __shared__ floatx4 partial[kProjectionWaves][NT][64];
+    // Lane (g, t) of token tile c holds rows 4 g .. + 3 of token 16 c + t; the waves' column ranges meet here and
+    // are added in wave order by the first 256 threads.
+    __shared__ floatx4 partial[kWaves][NT][64];
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
         partial[wave][c][lane] = acc[c];
     }
     __syncthreads();
+    if (threadIdx.x >= 256) {
+        return;
+    }
     const int source_lane = threadIdx.x >> 2;
     const int v = threadIdx.x & 3;
     const int row = tile * kQ8TileRows + 4 * (source_lane >> 4) + v;
@@ -147,27 +265,186 @@ __global__ __launch_bounds__(kProjectionWaves * 64) void project_kernel(Projecti
         if (token >= a.tokens) {
             continue;
         }
-        const float sum = ((partial[0][c][source_lane][v] + partial[1][c][source_lane][v]) + partial[2][c][source_lane][v]) +
-                          partial[3][c][source_lane][v];
+        float sum = partial[0][c][source_lane][v];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+            sum += partial[w][c][source_lane][v];
+        }
         const float total = sum + bias;
         float* destination = a.output + static_cast<size_t>(token) * a.out_stride + seg.out_column + row;
         *destination = a.accumulate != 0 ? *destination + total : total;
     }
 }
 
+// ---- Decode (at most 16 tokens): row tiles share the split input through LDS ----------------------------------
+
+// A workgroup of four waves covers four 16-row tiles (one per wave; tiles of different matrices may meet in one
+// workgroup) over one slice of at most kDecodeSliceChunks column chunks. The workgroup first splits its slice of the
+// input into the three bf16 parts, in B-fragment order, into LDS; then every wave streams its tile's codes and
+// scales for the slice (its only vector-memory loads, all issued up front) and multiplies against the fragments in
+// LDS. Each slice's 16 x 16 sums go to partial rows; reduce_kernel adds the slices in order with the bias and the
+// residual. The input is read from L2 once per workgroup instead of once per tile.
+constexpr int kDecodeSliceChunks = 8;
+constexpr int kDecodeTiles = 4;
+
+__device__ inline int locate_tile(const ProjectionArgs& a, int tile, ProjectionSegment& seg) {
+    int s = 0;
+    while (s + 1 < a.segments && tile >= a.segment[s + 1].first_tile) {
+        ++s;
+    }
+    seg = a.segment[s];
+    return tile - seg.first_tile;
+}
+
+__global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(ProjectionArgs a) {
+    constexpr int kItems = kDecodeSliceChunks * 128 / (kDecodeTiles * 64);  // split items per thread
+    __shared__ bf16x8 staged[kDecodeSliceChunks * kParts * 2 * 64];
+    const int slice = blockIdx.y;
+    const int k0 = slice * a.chunks / a.slices;
+    const int k1 = (slice + 1) * a.chunks / a.slices;
+    const int count = k1 - k0;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    const int global_tile = min(blockIdx.x * kDecodeTiles + wave, a.total_tiles - 1);
+
+    // 1. This thread's input loads for the split: item = threadIdx.x + 256 j is (token item % 16, 8-column group
+    //    item / 16 of the slice). Tokens past the last and columns past the matrix read nothing (zeros).
+    floatx4 raw[kItems][2];
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+        const int item = threadIdx.x + j * kDecodeTiles * 64;
+        const int t = item & 15;
+        const int group = item >> 4;
+        const int column = (k0 + (group >> 3)) * kQ8ChunkColumns + 8 * (group & 7);
+        const bool inside = (group >> 3) < count && t < a.tokens && column < a.columns;
+        const floatx4* source = reinterpret_cast<const floatx4*>(
+            a.input + static_cast<size_t>(inside ? t : 0) * a.in_stride + (inside ? column : 0));
+        raw[j][0] = source[0];
+        raw[j][1] = source[1];
+        if (!inside) {
+            raw[j][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            raw[j][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    // 2. This wave's codes and scales for the slice, issued after the input loads: loads complete in issue order,
+    //    so the split below waits for the input only, while the weight stream stays in flight.
+    ProjectionSegment seg;
+    const int tile = locate_tile(a, global_tile, seg);
+    const uintx4* codes =
+        reinterpret_cast<const uintx4*>(seg.codes + (static_cast<size_t>(tile) * a.chunks + k0) * kQ8TileBytes) + lane;
+    const uintx4* scales =
+        reinterpret_cast<const uintx4*>(seg.scales + (static_cast<size_t>(tile) * a.chunks + k0) * kQ8TileScales) + g;
+    uintx4 batch_codes[kDecodeSliceChunks];
+    uintx4 batch_scales[kDecodeSliceChunks];
+#pragma unroll
+    for (int i = 0; i < kDecodeSliceChunks; ++i) {
+        const int chunk = min(i, count - 1);
+        batch_codes[i] = __builtin_nontemporal_load(codes + static_cast<size_t>(chunk) * 64);
+        batch_scales[i] = scales[static_cast<size_t>(chunk) * 4];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. Split into the three bf16 parts, in B-fragment order, into LDS.
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+        const int item = threadIdx.x + j * kDecodeTiles * 64;
+        const int t = item & 15;
+        const int group = item >> 4;
+        const int chunk = group >> 3;
+        const int within = 8 * (group & 7);  // column within the chunk
+        const int block = within / kQ8BlockElements;
+        const int lane_group = (within % kQ8BlockElements) / 8;
+        bf16x8 parts[kParts];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __bf16 hi;
+            __bf16 mid;
+            __bf16 lo;
+            split3(raw[j][i / 4][i % 4], hi, mid, lo);
+            parts[0][i] = hi;
+            parts[1][i] = mid;
+            parts[2][i] = lo;
+        }
+#pragma unroll
+        for (int p = 0; p < kParts; ++p) {
+            staged[((chunk * kParts + p) * 2 + block) * 64 + 16 * lane_group + t] = parts[p];
+        }
+    }
+    __syncthreads();
+
+    // 4. Multiply the slice against the staged input.
+    floatx4 acc[1] = {floatx4{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+    for (int i = 0; i < kDecodeSliceChunks; ++i) {
+        if (i < count) {
+            InputFragments<1> input;
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                for (int p = 0; p < kParts; ++p) {
+                    input.x[0][b][p] = staged[((i * kParts + p) * 2 + b) * 64 + lane];
+                }
+            }
+            multiply_chunk<1>(batch_codes[i], batch_scales[i], input, acc);
+        }
+    }
+    if (blockIdx.x * kDecodeTiles + wave >= a.total_tiles) {
+        return;  // a fourth tile past the last (it loaded the last tile again)
+    }
+    // Lane (g, t) holds rows 4 g .. + 3 of token t: partial[slice][t][16 * global_tile + 4 g + i].
+    const int t = lane & 15;
+    float* destination = a.partials + (static_cast<size_t>(slice) * 16 + t) * a.partial_stride +
+                         static_cast<size_t>(global_tile) * kQ8TileRows + 4 * g;
+    *reinterpret_cast<floatx4*>(destination) = acc[0];
+}
+
+// output[t][out_column + row] = (accumulate ? output : 0) + (sum over slices in order) + bias, one thread per
+// (token, row of all segments).
+__global__ __launch_bounds__(256) void reduce_kernel(ProjectionArgs a) {
+    const int index = blockIdx.x * 256 + threadIdx.x;
+    const int rows = a.total_tiles * kQ8TileRows;
+    if (index >= a.tokens * rows) {
+        return;
+    }
+    const int t = index / rows;
+    const int global_row = index % rows;
+    ProjectionSegment seg;
+    const int tile = locate_tile(a, global_row / kQ8TileRows, seg);
+    const int row = tile * kQ8TileRows + global_row % kQ8TileRows;
+    if (row >= seg.rows) {
+        return;
+    }
+    const float* partial = a.partials + static_cast<size_t>(t) * a.partial_stride + global_row;
+    float sum = partial[0];
+    for (int slice = 1; slice < a.slices; ++slice) {
+        sum += partial[static_cast<size_t>(slice) * 16 * a.partial_stride];
+    }
+    const float total = sum + (seg.bias != nullptr ? seg.bias[row] : 0.0f);
+    float* destination = a.output + static_cast<size_t>(t) * a.out_stride + seg.out_column + row;
+    *destination = a.accumulate != 0 ? *destination + total : total;
+}
+
 }  // namespace
 
 int projection_token_tiles(int tokens) { return tokens <= 16 ? 1 : 4; }
 
+int projection_decode_slices(int chunks) { return (chunks + kDecodeSliceChunks - 1) / kDecodeSliceChunks; }
+
 hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles) {
+    if (args.tokens <= 16) {
+        const dim3 grid((tiles + kDecodeTiles - 1) / kDecodeTiles, args.slices);
+        SYNAPSE_KV_LAUNCH(project_decode_kernel, grid, dim3(kDecodeTiles * 64), launch, args);
+        const int outputs = args.tokens * tiles * kQ8TileRows;
+        SYNAPSE_KV_LAUNCH(reduce_kernel, dim3((outputs + 255) / 256), dim3(256), (Launch{launch.stream, nullptr, nullptr}),
+                          args);
+        return hipGetLastError();
+    }
+    const int splits = args.tokens * (args.padded_columns / 8);
+    SYNAPSE_KV_LAUNCH(split_kernel, dim3((splits + 255) / 256), dim3(256), (Launch{launch.stream, nullptr, nullptr}),
+                      args);
     const int per_block = 16 * projection_token_tiles(args.tokens);
     const dim3 grid(tiles, (args.tokens + per_block - 1) / per_block);
-    const dim3 block(kProjectionWaves * 64);
-    if (per_block == 16) {
-        SYNAPSE_KV_LAUNCH(project_kernel<1>, grid, block, launch, args);
-    } else {
-        SYNAPSE_KV_LAUNCH(project_kernel<4>, grid, block, launch, args);
-    }
+    SYNAPSE_KV_LAUNCH(project_kernel<4>, grid, dim3(projection_waves<4>() * 64), launch, args);
     return hipGetLastError();
 }
 

@@ -38,12 +38,17 @@ struct SynapseKvWeights {
     size_t bytes = 0;
     std::vector<synapse_kv::DeviceMatrix> matrices;
     std::vector<const void*> checked_pointers;  // device addresses that passed the check, most recent first
+    __bf16* parts = nullptr;  // scratch: the split input (prompt runs) or the per-slice sums (decode)
+    size_t parts_bytes = 0;
 
     ~SynapseKvWeights() {
         if (memory != nullptr) {
             (void)hipSetDevice(device);
             (void)hipStreamSynchronize(stream);
             (void)hipFree(memory);
+        }
+        if (parts != nullptr) {
+            (void)hipFree(parts);
         }
     }
 };
@@ -180,6 +185,30 @@ void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const floa
     args.accumulate = static_cast<int32_t>(p.accumulate);
     args.input = input;
     args.output = output;
+    args.padded_columns = args.chunks * kQ8ChunkColumns;
+    args.total_tiles = tiles;
+    args.slices = projection_decode_slices(args.chunks);
+    args.partial_stride = static_cast<int64_t>(tiles) * kQ8TileRows;
+    // Scratch: decode keeps per-slice sums ([slices][16][rows]); prompt runs the input's bf16 split in whole 16-token
+    // tiles (the kernel reads every column of a tile; a token past the last only feeds an output that is never
+    // written).
+    const size_t needed =
+        p.tokens <= 16
+            ? static_cast<size_t>(args.slices) * 16 * args.partial_stride * sizeof(float)
+            : static_cast<size_t>((p.tokens + 15) / 16) * 16 * args.padded_columns * 3 * sizeof(__bf16);
+    if (needed > weights.parts_bytes) {
+        // Work already queued may still read the old scratch.
+        check_hip(hipStreamSynchronize(weights.stream), "drain before reallocation");
+        if (weights.parts != nullptr) {
+            check_hip(hipFree(weights.parts), "projection scratch");
+            weights.parts = nullptr;
+            weights.parts_bytes = 0;
+        }
+        check_hip(hipMalloc(reinterpret_cast<void**>(&weights.parts), needed), "projection scratch");
+        weights.parts_bytes = needed;
+    }
+    args.parts = weights.parts;
+    args.partials = reinterpret_cast<float*>(weights.parts);
     check_hip(launch_projection(Launch{weights.stream, nullptr, nullptr}, args, tiles), "projection");
 }
 

@@ -128,9 +128,13 @@ int main() {
             for (size_t i = 0; i < codes_size; ++i) { if (!seen[i] && codes[i]) { ++failures; } }
         }
     }
-    // Fragment order: lane 16 g + r holds row r, columns 16 g .. 16 g + 15 of the chunk, 16 bytes at lane * 16.
-    if (q8_code_offset(2, 3, 64 + 16 * 2 + 5) != (long long)(1 * 1024 + (16 * 2 + 3) * 16 + 5)) { ++failures; }
-    if (q8_scale_offset(2, 18, 3) != (long long)((1 * 2 + 1) * 32 + 16 + 2)) { ++failures; }
+    // Fragment order: lane 16 g + r holds row r, columns 8 g .. 8 g + 7 of the chunk's first block, then of its
+    // second block, 16 bytes at lane * 16.
+    if (q8_code_offset(2, 3, 64 + 8 * 2 + 5) != (long long)(1 * 1024 + (16 * 2 + 3) * 16 + 5)) { ++failures; }
+    if (q8_code_offset(2, 3, 64 + 32 + 8 * 1 + 7) != (long long)(1 * 1024 + (16 * 1 + 3) * 16 + 8 + 7)) { ++failures; }
+    // Scales: row 18 is row 2 of tile 1 (row group 0); block 3 is the second block of chunk 1.
+    if (q8_scale_offset(2, 18, 3) != (long long)((1 * 2 + 1) * 32 + 0 * 8 + 1 * 4 + 2)) { ++failures; }
+    if (q8_scale_offset(2, 13, 0) != (long long)(3 * 8 + 0 * 4 + 1)) { ++failures; }
     std::printf("%d\n", failures);
     return failures != 0;
 }
