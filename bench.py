@@ -505,7 +505,8 @@ def config_projection(args, torch) -> dict:
         "data": f"synthetic Q8_0 weights (numpy seed {SEED + 7}), 28 distinct layers; torch N(0,1) activations",
         "config": {"workload": "7B projections: QKV 4,608 x 3,584 with biases + o_proj 3,584 x 3,584 accumulating, "
                                "28 layers, 16 tokens", "decode_tokens": decode_tokens, "prompt_tokens": prompt_tokens},
-        "roofline": {"bound": "hbm", "kernel": "project_kernel<1> (QKV, 3 segments)", "achieved": round(qkv_gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": "project_decode_kernel + reduce_kernel (QKV, 3 segments)",
+                     "achieved": round(qkv_gbps, 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(qkv_gbps / PEAK_HBM_GBPS, 4),
                      "traffic": None, "algorithmic_bytes_per_launch": int(qkv_bytes),
                      "avg_launch_us": round(qkv_us, 2),

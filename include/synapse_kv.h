@@ -265,9 +265,9 @@ typedef struct SynapseKvProjection {
     uint32_t reserved;      /* 0 */
 } SynapseKvProjection;
 
-/* Runs a projection on the weights' stream (the matrix-vector kernel for decode tokens and the tiled GEMM for
- * prompt runs, project() in step/projection.rs:51-72, as one MFMA kernel); input and output are device pointers.
- * Output rows of different tokens must not overlap the input. */
+/* Runs a projection on the weights' stream (project() in step/projection.rs:51-72: up to 16 tokens take the
+ * decode kernels, longer runs the tiled GEMM); input and output are device pointers and must not overlap. The
+ * weights keep a scratch buffer for the call (per-slice sums or the split input), grown on demand. */
 int32_t synapse_kv_project(SynapseKvWeights* weights, const SynapseKvProjection* projection, const float* input,
                            float* output);
 

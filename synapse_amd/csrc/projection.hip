@@ -13,17 +13,16 @@
 // accumulator, and the block's sum is then scaled and added as the reference does (sum = fma(block dot, d, sum),
 // matmul.cu:101-104). Only the order of the FP32 additions differs from the reference's kernels.
 //
-// MI355X mapping: split_kernel writes the three parts of the input once per projection, in the B-operand fragment
-// order of the MFMA (zero past the matrix's columns and the last token). project_kernel: one workgroup per
-// (16-row tile, 16 * NT tokens);
-// the waves split the columns into contiguous ranges of 64-column chunks (two blocks). Per chunk a wave loads
-// its tile's 1 KiB of codes (one 16-byte load per lane, fragment order, see q8_layout.h), the scales of its
-// accumulator rows, and per token tile the six 16-byte B fragments (part x block); chunks are loaded in groups
-// ahead of the multiplies. The waves' 16 x 16 * NT sums meet in LDS and are added in wave order, then the bias
-// and the residual.
+// MI355X mapping, decode (at most 16 tokens): project_decode_kernel, one workgroup per four 16-row tiles and one
+// slice of at most eight 64-column chunks; the workgroup splits its input slice into LDS once and every wave streams
+// its tile's codes and scales against it (see below); reduce_kernel adds the slices in order with bias and residual.
 //
-// The same kernel serves decode (NT = 1: up to 16 tokens, the weight stream dominates) and prompt runs (NT = 4:
-// 64 tokens per workgroup, each weight tile converted once and used for four token tiles).
+// Prompt runs: split_kernel writes the three parts of the whole input once, in the B-operand fragment order of the
+// MFMA, and project_kernel<4> runs one workgroup per (16-row tile, 64 tokens); its four waves split the columns
+// into contiguous ranges of 64-column chunks and load, per chunk, the tile's 1 KiB of codes (one 16-byte load per
+// lane, fragment order, see q8_layout.h), the scales of their accumulator rows and, per token tile, the six 16-byte
+// B fragments (part x block), in batches ahead of the multiplies. The waves' 16 x 64 sums meet in LDS and are added
+// in wave order, then the bias and the residual.
 
 #include "kv_internal.h"
 #include "q8_layout.h"
@@ -36,12 +35,10 @@ typedef uint32_t uintx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t uintx2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// Waves per workgroup (each takes an equal contiguous range of the column chunks): eight for decode, so a SIMD
-// holds about two waves of a layer-sized launch and one wave's loads hide behind another's multiplies; four for
-// prompt runs, whose workgroups already fill the device.
+// Waves per workgroup of project_kernel; each takes an equal contiguous range of the column chunks.
 template <int NT>
 constexpr int projection_waves() {
-    return NT == 1 ? 8 : 4;
+    return 4;
 }
 constexpr int kParts = 3;
 
@@ -119,10 +116,10 @@ struct InputFragments {
 
 // Chunks per batch: a batch's loads are all issued (in the order the multiplies use them: each chunk's input
 // fragments, then its codes and scales) before its first multiply. Vector memory loads complete in issue order, so
-// a batch is one round trip; a second wave on the SIMD overlaps its own round trip with this wave's multiplies.
+// a batch is one round trip; another wave on the SIMD overlaps its own round trip with this wave's multiplies.
 template <int NT>
 constexpr int projection_batch() {
-    return NT == 1 ? 7 : 2;
+    return 2;
 }
 
 // One chunk (two blocks): each block's three part products go to their own fresh accumulator, issued part by part
