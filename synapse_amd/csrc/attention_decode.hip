@@ -245,30 +245,27 @@ __device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, 
             step_f16<D>(fragments, query, state, key0, key_end, a.scale_log2);
         }
     } else {
-        // Two register sets: the loads of the next step are in flight while the current step computes.
+        // Two register sets: the loads of the next step are in flight while the current step computes. The loop
+        // runs while at least two steps remain, so both of its fetches are unconditional and every step waits only
+        // for its own fragments (a fetch under a branch would leave the number of loads in flight unknown at the
+        // join, and the step after it would wait for the prefetched block too); the last one or two steps follow.
         Fragments16<D> even;
         Fragments16<D> odd;
         int key0 = key_begin;
         fetch_f16<D>(geo, table, key_region, value_region, key0, even);
-        while (true) {
-            const bool more = key0 + kStepKeys < key_end;
-            if (more) {
-                fetch_f16<D>(geo, table, key_region, value_region, key0 + kStepKeys, odd);
-            }
+        while (key0 + 2 * kStepKeys < key_end) {
+            fetch_f16<D>(geo, table, key_region, value_region, key0 + kStepKeys, odd);
             step_f16<D>(even, query, state, key0, key_end, a.scale_log2);
-            if (!more) {
-                break;
-            }
-            key0 += kStepKeys;
-            const bool after = key0 + kStepKeys < key_end;
-            if (after) {
-                fetch_f16<D>(geo, table, key_region, value_region, key0 + kStepKeys, even);
-            }
-            step_f16<D>(odd, query, state, key0, key_end, a.scale_log2);
-            if (!after) {
-                break;
-            }
-            key0 += kStepKeys;
+            fetch_f16<D>(geo, table, key_region, value_region, key0 + 2 * kStepKeys, even);
+            step_f16<D>(odd, query, state, key0 + kStepKeys, key_end, a.scale_log2);
+            key0 += 2 * kStepKeys;
+        }
+        if (key0 + kStepKeys < key_end) {
+            fetch_f16<D>(geo, table, key_region, value_region, key0 + kStepKeys, odd);
+            step_f16<D>(even, query, state, key0, key_end, a.scale_log2);
+            step_f16<D>(odd, query, state, key0 + kStepKeys, key_end, a.scale_log2);
+        } else {
+            step_f16<D>(even, query, state, key0, key_end, a.scale_log2);
         }
     }
 }
@@ -479,7 +476,15 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
     const int first = a.worker_segments[worker];
     const int last = a.worker_segments[worker + 1];
     for (int index = first; index < last; ++index) {
-        const DecodeSegment seg = a.segments[index];
+        // Every lane reads the same segment: its fields are made uniform so the key loops branch on scalars.
+        const DecodeSegment loaded = a.segments[index];
+        DecodeSegment seg;
+        seg.token = __builtin_amdgcn_readfirstlane(loaded.token);
+        seg.kv_head = __builtin_amdgcn_readfirstlane(loaded.kv_head);
+        seg.key_begin = __builtin_amdgcn_readfirstlane(loaded.key_begin);
+        seg.key_end = __builtin_amdgcn_readfirstlane(loaded.key_end);
+        seg.row = __builtin_amdgcn_readfirstlane(loaded.row);
+        seg.merge = __builtin_amdgcn_readfirstlane(loaded.merge);
         if (a.append && seg.key_end == a.tokens[seg.token].position + 1) {
             if constexpr (F16) {
                 append_row<_Float16, D>(a, seg);
