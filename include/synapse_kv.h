@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 /* ABI version checked by the loader before any other call (ffi.rs:12 ABI_VERSION; NativeGpuLibrary.cs:14). */
-#define SYNAPSE_KV_ABI_VERSION 2u
+#define SYNAPSE_KV_ABI_VERSION 3u
 
 /* Status codes, identical to error.rs:4-16. */
 #define SYNAPSE_KV_OK 0
@@ -107,6 +107,7 @@ typedef struct SynapseKvPageStats {
 #define SYNAPSE_KV_KERNEL_MERGE 4   /* split merge */
 #define SYNAPSE_KV_KERNEL_PREFILL 5 /* prompt-run attention, and shared-prefix pages read once for their sharers */
 #define SYNAPSE_KV_KERNEL_GATHER 6  /* KV read-back */
+#define SYNAPSE_KV_KERNEL_PAGE_SELECT 7 /* KV page activation: key summaries and page selection */
 typedef struct SynapseKvProfile {
     uint64_t launches[8];
     double milliseconds[8];
@@ -161,6 +162,33 @@ int32_t synapse_kv_fork(SynapseKvCache* cache, uint32_t source, uint32_t target)
  * the tokens (validate_step, decoder.rs:303-335), grows slots and copies shared pages on write, and uploads the
  * tokens and the attention work plan. `tokens` is a host array. */
 int32_t synapse_kv_step(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count);
+
+/* synapse_kv_step with the step's prompt boundary (IBatchDecoder.Forward(tokens, promptStart),
+ * BatchDecoding.cs:10-33): tokens from `prompt_start` on are prompt tokens and attend densely under KV page
+ * activation. synapse_kv_step is this call with prompt_start = count. */
+int32_t synapse_kv_step_prompt(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count,
+                               size_t prompt_start);
+
+/* Query-aware KV page activation (ADR-016; KvPageActivation.cs, KvPageSelector.cs:17-54, Qwen2KvPageMasks.cs):
+ * a decode unit (a token before the prompt boundary that is alone in its slot in the step) attends, per KV head,
+ * to the sink page (positions 0..page_tokens-1), the pages overlapping its last window_tokens positions, and
+ * budget_pages more pages: those with the highest bound max over the group's query heads of
+ * sum_d max(q_d * min_d, q_d * max_d) over the page's per-channel key minimum and maximum (KEY_BOUND), or a seeded
+ * random draw (RANDOM, the control; seed per (layer, KV head, position) as Qwen2KvPageMasks). Unselected pages
+ * contribute nothing to that step's softmax. An approximation: off (enabled = 0) by default. Enabling builds the
+ * per-page key summaries of everything already cached; later appends keep them current. */
+#define SYNAPSE_KV_SELECT_KEY_BOUND 0u
+#define SYNAPSE_KV_SELECT_RANDOM 1u
+typedef struct SynapseKvPageActivation {
+    uint32_t enabled;       /* 0: dense attention (default) */
+    uint32_t budget_pages;  /* BudgetPages */
+    uint32_t window_tokens; /* WindowTokens */
+    uint32_t page_tokens;   /* PageTokens: 64 here (16 and 32 are UNAVAILABLE) */
+    uint32_t selection;     /* SYNAPSE_KV_SELECT_* */
+    int32_t seed;           /* Seed of the random control */
+} SynapseKvPageActivation;
+
+int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPageActivation* activation);
 
 /* synapse_rope_kv[_f16] for one layer of the current step (elementwise.metal:73-126; dispatch step/layers.rs:
  * 111-148): `qkv` is a device [tokens][qkv_stride] FP32 block with Q at column 0, K at heads*head_dim and V at
@@ -284,6 +312,7 @@ static_assert(sizeof(SynapseKvDesc) == 64, "SynapseKvDesc is pinned at 64 bytes"
 static_assert(sizeof(SynapseKvPageStats) == 40, "SynapseKvPageStats is pinned at 40 bytes");
 static_assert(sizeof(SynapseKvProfile) == 128, "SynapseKvProfile is pinned at 128 bytes");
 static_assert(sizeof(SynapseKvMatrix) == 24, "SynapseKvMatrix is pinned at 24 bytes");
+static_assert(sizeof(SynapseKvPageActivation) == 24, "SynapseKvPageActivation is pinned at 24 bytes");
 static_assert(sizeof(SynapseKvProjection) == 48, "SynapseKvProjection is pinned at 48 bytes");
 #else
 _Static_assert(sizeof(SynapseKvDeviceInfo) == 152, "SynapseKvDeviceInfo is pinned at 152 bytes");
@@ -292,6 +321,7 @@ _Static_assert(sizeof(SynapseKvDesc) == 64, "SynapseKvDesc is pinned at 64 bytes
 _Static_assert(sizeof(SynapseKvPageStats) == 40, "SynapseKvPageStats is pinned at 40 bytes");
 _Static_assert(sizeof(SynapseKvProfile) == 128, "SynapseKvProfile is pinned at 128 bytes");
 _Static_assert(sizeof(SynapseKvMatrix) == 24, "SynapseKvMatrix is pinned at 24 bytes");
+_Static_assert(sizeof(SynapseKvPageActivation) == 24, "SynapseKvPageActivation is pinned at 24 bytes");
 _Static_assert(sizeof(SynapseKvProjection) == 48, "SynapseKvProjection is pinned at 48 bytes");
 #endif
 

@@ -289,12 +289,15 @@ const float* value_row(const KeyView& view, int position, int kv_head) {
 }
 
 // Qwen2CpuAttention.Attend for one (token, head) item (Qwen2CpuAttention.cs:82-113) with its Softmax (:152-172,
-// multiply by 1/sum) and MultiplyAdd (:135-149). `scores` must hold position + 1 floats.
+// multiply by 1/sum) and MultiplyAdd (:135-149). `scores` must hold position + 1 floats. `attended` (null: every
+// position) is a KV page mask: unattended positions score -infinity and add no value.
 void attend_managed(const KeyView& view, const float* query, int kv_head, int position, float scale, float* scores,
-                    float* destination) {
+                    float* destination, const uint8_t* attended = nullptr) {
     const int d = view.head_dim;
     for (int cached = 0; cached <= position; ++cached) {
-        scores[cached] = dot_lanes(query, key_row(view, cached, kv_head), d) * scale;
+        scores[cached] = attended == nullptr || attended[cached]
+                             ? dot_lanes(query, key_row(view, cached, kv_head), d) * scale
+                             : -std::numeric_limits<float>::infinity();
     }
     float maximum = scores[0];
     for (int index = 1; index <= position; ++index) {
@@ -313,6 +316,9 @@ void attend_managed(const KeyView& view, const float* query, int kv_head, int po
         destination[dim] = 0.0f;
     }
     for (int cached = 0; cached <= position; ++cached) {
+        if (attended != nullptr && !attended[cached]) {
+            continue;
+        }
         const float* value = value_row(view, cached, kv_head);
         const float weight = scores[cached];
         for (int dim = 0; dim < d; ++dim) {
@@ -995,12 +1001,279 @@ void orc_attention_split(const float* query, const float* keys, const float* val
     }
 }
 
+}  // extern "C"
+
+// ---- Query-aware KV page activation (ADR-016) ----------------------------------------------------------------
+
+namespace {
+
+// System.Random(int seed), the seeded generator .NET keeps for compatibility (dotnet/runtime
+// src/libraries/System.Private.CoreLib/src/System/Random.Net5CompatImpl.cs, CompatPrng): Knuth's subtractive
+// generator (TAOCP vol. 2, 3.6) as Numerical Recipes' ran3 seeds it, 55 words, lag 21 between the two indices.
+// Not part of the reference tree; KvPageSelector.RandomPages (KvPageSelector.cs:118-129) draws from it.
+struct CompatRandom {
+    static constexpr int32_t kBig = 2147483647;  // int.MaxValue
+    int32_t words[56];
+    int first = 0;
+    int second = 21;
+
+    explicit CompatRandom(int32_t seed) {
+        int32_t previous = 161803398 - (seed == INT32_MIN ? kBig : std::abs(seed));
+        words[55] = previous;
+        int32_t current = 1;
+        for (int i = 1, at = 0; i < 55; ++i) {
+            at = (at + 21) % 55;
+            words[at] = current;
+            current = previous - current;
+            if (current < 0) {
+                current += kBig;
+            }
+            previous = words[at];
+        }
+        for (int pass = 0; pass < 4; ++pass) {
+            for (int i = 1; i < 56; ++i) {
+                words[i] -= words[1 + (i + 30) % 55];
+                if (words[i] < 0) {
+                    words[i] += kBig;
+                }
+            }
+        }
+    }
+
+    // InternalSample; Random.Next() returns it as is.
+    int32_t sample() {
+        first = first + 1 >= 56 ? 1 : first + 1;
+        second = second + 1 >= 56 ? 1 : second + 1;
+        int32_t value = words[first] - words[second];
+        if (value == kBig) {
+            value -= 1;
+        }
+        if (value < 0) {
+            value += kBig;
+        }
+        words[first] = value;
+        return value;
+    }
+
+    // Next(minValue, maxValue) for maxValue - minValue <= int.MaxValue: truncation of Sample() * range.
+    int32_t next(int32_t low, int32_t high) {
+        const double unit = sample() * (1.0 / kBig);
+        return static_cast<int32_t>(unit * (static_cast<int64_t>(high) - low)) + low;
+    }
+};
+
+// MathF.Min / MathF.Max (System.MathF): a NaN operand wins, and -0 < +0.
+float math_f_min(float x, float y) {
+    if (x != y) {
+        return std::isnan(x) ? x : (x < y ? x : y);
+    }
+    return std::signbit(x) ? x : y;
+}
+
+float math_f_max(float x, float y) {
+    if (x != y) {
+        return std::isnan(x) ? x : (y < x ? x : y);
+    }
+    return std::signbit(y) ? x : y;
+}
+
+// float.CompareTo: NaN sorts below every number and equals NaN.
+int float_compare(float x, float y) {
+    if (x < y) {
+        return -1;
+    }
+    if (x > y) {
+        return 1;
+    }
+    if (x == y) {
+        return 0;
+    }
+    return std::isnan(x) ? (std::isnan(y) ? 0 : -1) : 1;
+}
+
+struct Activation {
+    int32_t budget_pages;
+    int32_t window_tokens;
+    int32_t page_tokens;
+    int32_t selection;  // 0 key bound, 1 random
+    int32_t seed;
+};
+
+// A key reader: keys of one KV head, row `position` at keys + position * stride.
+struct Keys {
+    const float* base;
+    size_t stride;
+    const float* at(int position) const { return base + static_cast<size_t>(position) * stride; }
+};
+
+// KvPageSelector.PageBound (KvPageSelector.cs:57-93).
+float page_bound(const float* queries, int group, int head_dim, const Keys& keys, int first, int last) {
+    std::vector<float> minimum(keys.at(first), keys.at(first) + head_dim);
+    std::vector<float> maximum(minimum);
+    for (int position = first + 1; position <= last; ++position) {
+        const float* key = keys.at(position);
+        for (int channel = 0; channel < head_dim; ++channel) {
+            minimum[channel] = math_f_min(minimum[channel], key[channel]);
+            maximum[channel] = math_f_max(maximum[channel], key[channel]);
+        }
+    }
+    float best = -std::numeric_limits<float>::infinity();
+    for (int head = 0; head < group; ++head) {
+        const float* query = queries + static_cast<size_t>(head) * head_dim;
+        float bound = 0.0f;
+        for (int channel = 0; channel < head_dim; ++channel) {
+            const float low = query[channel] * minimum[channel];
+            const float high = query[channel] * maximum[channel];
+            bound += math_f_max(low, high);
+        }
+        best = math_f_max(best, bound);
+    }
+    return best;
+}
+
+void mark_page(uint8_t* selected, int page, int size, int position) {
+    const int first = page * size;
+    const int last = std::min(first + size - 1, position);
+    for (int index = first; index <= last; ++index) {
+        selected[index] = 1;
+    }
+}
+
+// KvPageSelector.Select (KvPageSelector.cs:17-54) with BestPages (:96-115) and RandomPages (:118-129).
+void page_select(const Activation& activation, const float* queries, int group, int head_dim, const Keys& keys,
+                 int position, int32_t seed, uint8_t* selected) {
+    const int count = position + 1;
+    const int size = activation.page_tokens;
+    std::fill(selected, selected + count, 0);
+    const int window_page = std::max(0, count - activation.window_tokens) / size;
+    mark_page(selected, 0, size, position);
+    for (int page = window_page; page <= position / size; ++page) {
+        mark_page(selected, page, size, position);
+    }
+    const int candidates = std::max(0, window_page - 1);
+    if (candidates <= activation.budget_pages) {
+        for (int page = 1; page < window_page; ++page) {
+            mark_page(selected, page, size, position);
+        }
+        return;
+    }
+    std::vector<int> chosen;
+    if (activation.selection == 1) {
+        std::vector<int> pages(candidates);
+        for (int index = 0; index < candidates; ++index) {
+            pages[index] = index + 1;
+        }
+        CompatRandom random(seed);
+        for (int index = 0; index < activation.budget_pages; ++index) {
+            std::swap(pages[index], pages[random.next(index, candidates)]);
+        }
+        chosen.assign(pages.begin(), pages.begin() + activation.budget_pages);
+    } else {
+        std::vector<std::pair<float, int>> ranked(candidates);
+        for (int page = 1; page <= candidates; ++page) {
+            const int first = page * size;
+            ranked[page - 1] = {page_bound(queries, group, head_dim, keys, first, first + size - 1), page};
+        }
+        std::sort(ranked.begin(), ranked.end(), [](const auto& left, const auto& right) {
+            const int order = float_compare(right.first, left.first);
+            return order != 0 ? order < 0 : left.second < right.second;
+        });
+        for (int index = 0; index < activation.budget_pages; ++index) {
+            chosen.push_back(ranked[index].second);
+        }
+    }
+    for (int page : chosen) {
+        mark_page(selected, page, size, position);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+// Random(seed).Next() `count` times (low == high == 0) or Next(low, high) `count` times.
+void orc_dotnet_random(int32_t seed, int count, int32_t low, int32_t high, int32_t* out) {
+    CompatRandom random(seed);
+    for (int index = 0; index < count; ++index) {
+        out[index] = low == 0 && high == 0 ? random.sample() : random.next(low, high);
+    }
+}
+
+float orc_page_bound(const float* queries, int group, int head_dim, const float* keys, int first, int last) {
+    return page_bound(queries, group, head_dim, Keys{keys, static_cast<size_t>(head_dim)}, first, last);
+}
+
+// KvPageSelector.Select over keys [positions][head_dim] of one KV head; selected[0..position].
+void orc_page_select(int budget_pages, int window_tokens, int page_tokens, int selection, const float* queries,
+                     int group, int head_dim, const float* keys, int position, int32_t seed, uint8_t* selected) {
+    const Activation activation{budget_pages, window_tokens, page_tokens, selection, 0};
+    page_select(activation, queries, group, head_dim, Keys{keys, static_cast<size_t>(head_dim)}, position, seed,
+                selected);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Qwen2KvPageMasks.Prepare (Qwen2KvPageMasks.cs:21-54): for each decode unit (a token before prompt_start alone in
+// its slot) and KV head, the selected positions; masks[(token * kv_heads + kv_head) * stride + position], and
+// units[token] = 1 for a decode unit.
+void page_masks(const Activation& activation, int layer, const int32_t* step, int count, int prompt_start,
+                const float* qkv, int qkv_stride, int kv_heads, int group, int head_dim,
+                const std::vector<std::vector<float>>& keys, size_t stride, std::vector<uint8_t>& masks,
+                std::vector<uint8_t>& units) {
+    units.assign(count, 0);
+    masks.assign(static_cast<size_t>(count) * kv_heads * stride, 0);
+    for (int token = 0; token < count; ++token) {
+        const int slot = step[4 * token];
+        bool dense = token >= prompt_start;
+        for (int other = 0; other < count && !dense; ++other) {
+            dense = other != token && step[4 * other] == slot;
+        }
+        if (dense) {
+            continue;
+        }
+        units[token] = 1;
+        const int position = step[4 * token + 2];
+        for (int kv_head = 0; kv_head < kv_heads; ++kv_head) {
+            const uint32_t seed = static_cast<uint32_t>(activation.seed) * 1000003u +
+                                  static_cast<uint32_t>(layer) * 7919u + static_cast<uint32_t>(kv_head) * 104729u +
+                                  static_cast<uint32_t>(position);
+            const Keys reader{keys[slot].data() + static_cast<size_t>(kv_head) * head_dim,
+                              static_cast<size_t>(kv_heads) * head_dim};
+            page_select(activation, qkv + static_cast<size_t>(token) * qkv_stride +
+                                        static_cast<size_t>(kv_head) * group * head_dim,
+                        group, head_dim, reader, position, static_cast<int32_t>(seed),
+                        masks.data() + (static_cast<size_t>(token) * kv_heads + kv_head) * stride);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
 // Decode/prefill attention of the prepared step for one layer, read through the paged cache:
 // Qwen2CpuAttention.Execute (Qwen2CpuAttention.cs:55-79) with its (token, head) work items spread over `threads`
 // std::threads. q rows at qkv + token * qkv_stride (heads * head_dim floats), outputs at out + token * out_stride.
+// With `activation` (budget, window, page_tokens, selection, seed; null: dense) the decode units of the step attend
+// only their selected positions (Qwen2KvPageMasks; Qwen2CpuAttention.Attend, :94-110); `selected`, when not null,
+// receives the masks as [token][kv_head][maximum positions] bytes (all zero for dense tokens).
 // Returns the wall time of the attention in seconds (the gather of FP16 pages to FP32 is not timed).
+double orc_paged_attention_pages(void* handle, int layer, const float* qkv, int qkv_stride, float* output,
+                                 int out_stride, int threads, const int32_t* activation, int prompt_start,
+                                 uint8_t* selected);
+
 double orc_paged_attention(void* handle, int layer, const float* qkv, int qkv_stride, float* output, int out_stride,
                            int threads) {
+    const auto& cache = *static_cast<PagedCache*>(handle);
+    return orc_paged_attention_pages(handle, layer, qkv, qkv_stride, output, out_stride, threads, nullptr,
+                                     static_cast<int>(cache.step.size() / 4), nullptr);
+}
+
+double orc_paged_attention_pages(void* handle, int layer, const float* qkv, int qkv_stride, float* output,
+                                 int out_stride, int threads, const int32_t* activation, int prompt_start,
+                                 uint8_t* selected) {
     auto& cache = *static_cast<PagedCache*>(handle);
     const int count = static_cast<int>(cache.step.size() / 4);
     const Token* tokens = reinterpret_cast<const Token*>(cache.step.data());
@@ -1027,6 +1300,17 @@ double orc_paged_attention(void* handle, int layer, const float* qkv, int qkv_st
     for (int slot = 0; slot < cache.max_sequences; ++slot) {
         longest = std::max(longest, extent[slot]);
     }
+    std::vector<uint8_t> masks;
+    std::vector<uint8_t> units(count, 0);
+    const size_t mask_stride = static_cast<size_t>(cache.maximum);
+    if (activation != nullptr) {
+        const Activation parsed{activation[0], activation[1], activation[2], activation[3], activation[4]};
+        page_masks(parsed, layer, cache.step.data(), count, prompt_start, qkv, qkv_stride, cache.kv_heads, group, d,
+                   keys, mask_stride, masks, units);
+        if (selected != nullptr) {
+            std::memcpy(selected, masks.data(), masks.size());
+        }
+    }
     const int workers = std::max(1, threads);
     std::vector<std::vector<float>> scores(workers, std::vector<float>(std::max(1, longest)));
     const auto start = std::chrono::steady_clock::now();
@@ -1035,9 +1319,12 @@ double orc_paged_attention(void* handle, int layer, const float* qkv, int qkv_st
         const int head = item % cache.heads;
         const Token token = tokens[index];
         const KeyView view{keys[token.slot].data(), values[token.slot].data(), cache.kv_heads, d};
+        const uint8_t* attended =
+            units[index] ? masks.data() + (static_cast<size_t>(index) * cache.kv_heads + head / group) * mask_stride
+                         : nullptr;
         attend_managed(view, qkv + static_cast<size_t>(index) * qkv_stride + static_cast<size_t>(head) * d,
                        head / group, token.position, scale, scores[worker].data(),
-                       output + static_cast<size_t>(index) * out_stride + static_cast<size_t>(head) * d);
+                       output + static_cast<size_t>(index) * out_stride + static_cast<size_t>(head) * d, attended);
     });
     return std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
 }

@@ -230,19 +230,26 @@ __device__ inline void step_f16(const Fragments16<D>& fragments, const half8 (&q
     }
 }
 
-// Keys [key_begin, key_end) of one KV head through the block table `table` against one column tile of queries,
-// FP16 pages. With PREFETCH the next step's fragments are loaded before the current step is computed.
+// Steps [step_begin, step_end) of one KV head through the block table `table` against one column tile of queries,
+// FP16 pages: step s covers the 64 keys of block `list[s]` (KV page activation) or of block s (list null); keys at
+// or past `key_limit` are masked. The list is read with uniform (scalar) loads. With PREFETCH the next step's
+// fragments are loaded before the current step is computed.
 template <int D, bool PREFETCH>
-__device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, int kv_head, int key_begin,
-                                  int key_end, const half8 (&query)[D / 32], WaveState<D>& state) {
+__device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, int kv_head, int step_begin,
+                                  int step_end, const int32_t* list, int key_limit, const half8 (&query)[D / 32],
+                                  WaveState<D>& state) {
     const Geometry& geo = a.geo;
     const size_t key_region = region_offset(geo, 0, kv_head);
     const size_t value_region = region_offset(geo, 1, kv_head);
+    auto first_key = [&](int step) __attribute__((always_inline)) {
+        return (list != nullptr ? list[step] : step) * kStepKeys;
+    };
     if constexpr (!PREFETCH) {
-        for (int key0 = key_begin; key0 < key_end; key0 += kStepKeys) {
+        for (int step = step_begin; step < step_end; ++step) {
             Fragments16<D> fragments;
+            const int key0 = first_key(step);
             fetch_f16<D>(geo, table, key_region, value_region, key0, fragments);
-            step_f16<D>(fragments, query, state, key0, key_end, a.scale_log2);
+            step_f16<D>(fragments, query, state, key0, key_limit, a.scale_log2);
         }
     } else {
         // Two register sets: the loads of the next step are in flight while the current step computes. The loop
@@ -251,37 +258,46 @@ __device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, 
         // join, and the step after it would wait for the prefetched block too); the last one or two steps follow.
         Fragments16<D> even;
         Fragments16<D> odd;
-        int key0 = key_begin;
+        int step = step_begin;
+        int key0 = first_key(step);
         fetch_f16<D>(geo, table, key_region, value_region, key0, even);
-        while (key0 + 2 * kStepKeys < key_end) {
-            fetch_f16<D>(geo, table, key_region, value_region, key0 + kStepKeys, odd);
-            step_f16<D>(even, query, state, key0, key_end, a.scale_log2);
-            fetch_f16<D>(geo, table, key_region, value_region, key0 + 2 * kStepKeys, even);
-            step_f16<D>(odd, query, state, key0 + kStepKeys, key_end, a.scale_log2);
-            key0 += 2 * kStepKeys;
+        while (step + 2 < step_end) {
+            const int key1 = first_key(step + 1);
+            const int key2 = first_key(step + 2);
+            fetch_f16<D>(geo, table, key_region, value_region, key1, odd);
+            step_f16<D>(even, query, state, key0, key_limit, a.scale_log2);
+            fetch_f16<D>(geo, table, key_region, value_region, key2, even);
+            step_f16<D>(odd, query, state, key1, key_limit, a.scale_log2);
+            step += 2;
+            key0 = key2;
         }
-        if (key0 + kStepKeys < key_end) {
-            fetch_f16<D>(geo, table, key_region, value_region, key0 + kStepKeys, odd);
-            step_f16<D>(even, query, state, key0, key_end, a.scale_log2);
-            step_f16<D>(odd, query, state, key0 + kStepKeys, key_end, a.scale_log2);
+        if (step + 1 < step_end) {
+            const int key1 = first_key(step + 1);
+            fetch_f16<D>(geo, table, key_region, value_region, key1, odd);
+            step_f16<D>(even, query, state, key0, key_limit, a.scale_log2);
+            step_f16<D>(odd, query, state, key1, key_limit, a.scale_log2);
         } else {
-            step_f16<D>(even, query, state, key0, key_end, a.scale_log2);
+            step_f16<D>(even, query, state, key0, key_limit, a.scale_log2);
         }
     }
 }
 
-// One token's keys [key_begin, key_end) for one KV head, FP16 pages.
+// One token's segment for one KV head, FP16 pages.
 template <int D, bool PREFETCH>
 __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
     const Geometry& geo = a.geo;
     const int r = threadIdx.x & 15;
     half8 query[D / 32];
     load_query_f16<D>(a, seg.token, seg.kv_head * geo.group + (r < geo.group ? r : 0), r < geo.group, query);
-    const int32_t* table = geo.block_table + static_cast<size_t>(a.tokens[seg.token].slot) * geo.pages_per_slot;
-    attend_blocks_f16<D, PREFETCH>(a, table, seg.kv_head, seg.key_begin, seg.key_end, query, state);
+    const SynapseKvBatchToken token = a.tokens[seg.token];
+    const int32_t* table = geo.block_table + static_cast<size_t>(token.slot) * geo.pages_per_slot;
+    const int32_t* list = seg.list >= 0 ? a.lists + seg.list : nullptr;
+    attend_blocks_f16<D, PREFETCH>(a, table, seg.kv_head, seg.key_begin / kStepKeys,
+                                   (seg.key_end + kStepKeys - 1) / kStepKeys, list,
+                                   list != nullptr ? token.position + 1 : seg.key_end, query, state);
 }
 
-// One token's keys [key_begin, key_end) for one KV head, FP32 pages.
+// One token's segment for one KV head, FP32 pages.
 template <int D>
 __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
     const Geometry& geo = a.geo;
@@ -323,13 +339,18 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
             }
         }
     }
-    const int slot = a.tokens[seg.token].slot;
-    const int32_t* table = geo.block_table + static_cast<size_t>(slot) * geo.pages_per_slot;
+    const SynapseKvBatchToken token = a.tokens[seg.token];
+    const int32_t* table = geo.block_table + static_cast<size_t>(token.slot) * geo.pages_per_slot;
     const size_t key_region = region_offset(geo, 0, seg.kv_head);
     const size_t value_region = region_offset(geo, 1, seg.kv_head);
     const int page_tokens = geo.page_tokens;
+    // Step s covers block list[s] under KV page activation, block s otherwise; keys at or past key_limit are masked.
+    const int32_t* list = seg.list >= 0 ? a.lists + seg.list : nullptr;
+    const int key_limit = list != nullptr ? token.position + 1 : seg.key_end;
+    const int step_end = (seg.key_end + kStepKeys - 1) / kStepKeys;
 
-    for (int key0 = seg.key_begin; key0 < seg.key_end; key0 += kStepKeys) {
+    for (int step = seg.key_begin / kStepKeys; step < step_end; ++step) {
+        const int key0 = (list != nullptr ? list[step] : step) * kStepKeys;
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
         const float* page =
@@ -376,7 +397,7 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int key = key0 + 16 * t + 4 * g + i;
-                scores[t][i] = key < seg.key_end ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
+                scores[t][i] = key < key_limit ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
             }
         }
         const float alpha = softmax_step(scores, state.maximum, state.sum);
@@ -485,7 +506,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
         seg.key_end = __builtin_amdgcn_readfirstlane(loaded.key_end);
         seg.row = __builtin_amdgcn_readfirstlane(loaded.row);
         seg.merge = __builtin_amdgcn_readfirstlane(loaded.merge);
-        if (a.append && seg.key_end == a.tokens[seg.token].position + 1) {
+        seg.list = __builtin_amdgcn_readfirstlane(loaded.list);
+        seg.last = __builtin_amdgcn_readfirstlane(loaded.last);
+        if (a.append && seg.last) {
             if constexpr (F16) {
                 append_row<_Float16, D>(a, seg);
             } else {

@@ -112,6 +112,75 @@ struct Uploader {
     }
 };
 
+// System.Random(int seed) as .NET seeds it (the runtime's compatible seeded generator, Random.Net5CompatImpl.cs:
+// Knuth's subtractive generator, Seminumerical Algorithms 3.6, in the Numerical Recipes "ran3" form with the
+// second index starting at 21), which KvPageSelector.RandomPages (KvPageSelector.cs:118-129) draws from. Only the
+// calls that path makes: the constructor and Next(minValue, maxValue) for ranges below 2^31.
+class SeededRandom {
+public:
+    explicit SeededRandom(int32_t seed) {
+        constexpr int32_t kSeed = 161803398;
+        const int32_t subtraction = seed == INT32_MIN ? INT32_MAX : (seed < 0 ? -seed : seed);
+        int32_t mj = kSeed - subtraction;
+        state_[55] = mj;
+        int32_t mk = 1;
+        int ii = 0;
+        for (int i = 1; i < 55; ++i) {
+            ii += 21;
+            if (ii >= 55) {
+                ii -= 55;
+            }
+            state_[ii] = mk;
+            mk = mj - mk;
+            if (mk < 0) {
+                mk += INT32_MAX;
+            }
+            mj = state_[ii];
+        }
+        for (int round = 1; round < 5; ++round) {
+            for (int i = 1; i < 56; ++i) {
+                int n = i + 30;
+                if (n >= 55) {
+                    n -= 55;
+                }
+                state_[i] -= state_[1 + n];
+                if (state_[i] < 0) {
+                    state_[i] += INT32_MAX;
+                }
+            }
+        }
+    }
+
+    // Next(minValue, maxValue): minValue + (int)(Sample() * (maxValue - minValue)).
+    int32_t next(int32_t minimum, int32_t maximum) {
+        const double sample = static_cast<double>(internal_sample()) * (1.0 / INT32_MAX);
+        return static_cast<int32_t>(sample * (static_cast<int64_t>(maximum) - minimum)) + minimum;
+    }
+
+private:
+    int32_t internal_sample() {
+        if (++next_ >= 56) {
+            next_ = 1;
+        }
+        if (++next_p_ >= 56) {
+            next_p_ = 1;
+        }
+        int32_t value = state_[next_] - state_[next_p_];
+        if (value == INT32_MAX) {
+            --value;
+        }
+        if (value < 0) {
+            value += INT32_MAX;
+        }
+        state_[next_] = value;
+        return value;
+    }
+
+    int32_t state_[56] = {};
+    int next_ = 0;
+    int next_p_ = 21;
+};
+
 struct Dims {
     uint32_t layers;
     uint32_t heads;
@@ -141,6 +210,9 @@ struct SynapseKvCache {
     int32_t prefill_slots = 256;         // resident prefill workgroups on the device
     uint32_t prefetch = 1;  // decode kernel variant: 1 = two register sets, next step's loads in flight
     uint32_t shared_prefix = 1;  // 1: decode reads copy-on-write pages shared by several step tokens once
+    SynapseKvPageActivation activation{};  // KV page activation (enabled = 0: dense)
+    synapse_kv::DeviceBuffer<uint8_t> summaries;  // per pool page: key minima and maxima of its 64-key blocks
+    uint64_t summary_page_bytes = 0;
 
     // Host shadow of the allocator (same rules as the table kernel).
     std::vector<uint32_t> capacity;
@@ -197,6 +269,13 @@ struct SynapseKvCache {
     size_t segments_offset = 0;
     size_t merges_offset = 0;
     size_t prefill_offset = 0;
+    int32_t prompt_start = 0;        // tokens from here on are prompt tokens (dense under page activation)
+    size_t lists_offset = 0;         // block lists of page-activated rows
+    size_t list_layer_entries = 0;   // entries per layer in the blob (random lists differ per layer), else 0
+    size_t select_offset = 0;        // key-bound selection jobs
+    int32_t select_jobs = 0;
+    size_t touched_offset = 0;       // (page, block) pairs the step writes: summaries recomputed after appends
+    int32_t touched_blocks = 0;
 
     ~SynapseKvCache() {
         (void)hipSetDevice(device);
@@ -218,6 +297,7 @@ struct SynapseKvCache {
         blob.reset();
         partial_out.reset();
         partial_ml.reset();
+        summaries.reset();
         if (pool != nullptr) {
             (void)hipFree(pool);
         }
@@ -339,6 +419,13 @@ void flush_ops(SynapseKvCache& cache) {
     check_hip(launch_zero_pages(launch_for(cache, SYNAPSE_KV_KERNEL_PAGES, zero.count > 0), zero), "zero pages");
     PageArgs copy{cache.pool, cache.dims.page_bytes, cache.copies.pointer, cache.copy_count};
     check_hip(launch_copy_pages(launch_for(cache, SYNAPSE_KV_KERNEL_PAGES, copy.count > 0), copy), "copy pages");
+    if (cache.activation.enabled != 0) {
+        // A copied page keeps its blocks' summaries (the step's writes into it recompute theirs afterwards).
+        PageArgs summary_copy{cache.summaries.pointer, cache.summary_page_bytes, cache.copies.pointer,
+                              cache.copy_count};
+        check_hip(launch_copy_pages(launch_for(cache, SYNAPSE_KV_KERNEL_PAGES, summary_copy.count > 0), summary_copy),
+                  "copy summaries");
+    }
     cache.ops.clear();
     cache.fresh_count = 0;
     cache.copy_count = 0;
@@ -431,6 +518,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         int64_t steps;
         size_t first_segment;
         int32_t pieces;
+        int32_t list;  // >= 0: the row's block list (KV page activation); keys counts list entries times 64
     };
     std::vector<PrefillItem> prefill;
     std::vector<MergeItem> prefill_merges;
@@ -454,6 +542,45 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         start = end;
     }
 
+    // KV page activation (Qwen2KvPageMasks.cs:21-54): a decode unit is a token before the prompt boundary that is
+    // alone in its slot. KvPageSelector.Select (KvPageSelector.cs:17-54) with 64-position pages gives its row, per
+    // KV head, the sink block 0, `budget` blocks of 1 .. candidates (ranked by key bound on the device, or drawn
+    // here) and the window blocks window_page .. position / 64; when the budget covers every candidate the row is
+    // dense. Listed rows read their blocks through the decode kernel and take no part in shared-prefix sets.
+    struct Unit {
+        int32_t window_page;  // -1: dense
+        int32_t candidates;
+        int32_t entries;
+    };
+    const SynapseKvPageActivation& activation = cache.activation;
+    std::vector<Unit> units(count, Unit{-1, 0, 0});
+    if (activation.enabled != 0) {
+        std::vector<int32_t> in_slot(dims.slots, 0);
+        for (int32_t index = 0; index < count; ++index) {
+            ++in_slot[tokens[index].slot];
+        }
+        for (int32_t index = 0; index < std::min(count, cache.prompt_start); ++index) {
+            if (in_slot[tokens[index].slot] != 1) {
+                continue;
+            }
+            const int64_t keys = static_cast<int64_t>(tokens[index].position) + 1;
+            const int32_t window_page =
+                static_cast<int32_t>(std::max<int64_t>(0, keys - activation.window_tokens) / kStepKeys);
+            const int32_t candidates = std::max(0, window_page - 1);
+            if (static_cast<uint32_t>(candidates) <= activation.budget_pages) {
+                continue;
+            }
+            if (activation.selection == SYNAPSE_KV_SELECT_KEY_BOUND && candidates > kMaxSelectCandidates) {
+                fail(SYNAPSE_KV_UNAVAILABLE, "key-bound page selection ranks at most " +
+                                                 std::to_string(kMaxSelectCandidates) + " pages; token " +
+                                                 std::to_string(index) + " has " + std::to_string(candidates));
+            }
+            const int32_t own_page = tokens[index].position / kStepKeys;
+            units[index] = Unit{window_page, candidates,
+                                1 + static_cast<int32_t>(activation.budget_pages) + own_page - window_page + 1};
+        }
+    }
+
     // Shared prefixes (FP16): lone tokens whose block tables map their leading pages to the same physical pages
     // (copy-on-write forks) form sets of up to kPrefillTokens members. A set's shared pages are those all members
     // map alike, below every member's own position (whose page the step has already made private); listed prefill
@@ -468,7 +595,12 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         auto first_page = [&](int32_t index) {
             return cache.table[static_cast<size_t>(tokens[index].slot) * dims.pages_per_slot];
         };
-        std::vector<int32_t> order = lone;
+        std::vector<int32_t> order;
+        for (int32_t index : lone) {
+            if (units[index].window_page < 0) {
+                order.push_back(index);
+            }
+        }
         std::stable_sort(order.begin(), order.end(),
                          [&](int32_t x, int32_t y) { return first_page(x) < first_page(y); });
         const size_t most = static_cast<size_t>(kPrefillTokens);
@@ -507,14 +639,83 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         }
     }
 
-    // Rows: every lone token's (token, KV head) rows, from the token's shared keys on.
+    // Rows: every lone token's (token, KV head) rows, from the token's shared keys on; a listed row's steps are its
+    // list entries.
     std::vector<Row> rows;
+    int32_t list_entries = 0;
     for (int32_t index : lone) {
-        const int32_t keys = tokens[index].position + 1;
+        const Unit& unit = units[index];
+        const int32_t keys = unit.window_page >= 0 ? unit.entries * kStepKeys : tokens[index].position + 1;
         const int32_t key_begin = set_of[index] >= 0 ? sets[set_of[index]].shared_keys : 0;
         for (uint32_t kv_head = 0; kv_head < dims.kv_heads; ++kv_head) {
+            int32_t list = -1;
+            if (unit.window_page >= 0) {
+                list = list_entries;
+                list_entries += unit.entries;
+            }
             rows.push_back(Row{index, static_cast<int32_t>(kv_head), key_begin, keys, set_of[index], 0,
-                               (keys - key_begin + kStepKeys - 1) / kStepKeys, 0, 0});
+                               (keys - key_begin + kStepKeys - 1) / kStepKeys, 0, 0, list});
+        }
+    }
+
+    // Block lists: [sink block 0][budget blocks, ascending][window blocks]. Key-bound budget entries are written by
+    // the selection kernel of each layer (one list region serves every layer); random draws depend on the layer
+    // (seed = Seed * 1000003 + layer * 7919 + kv_head * 104729 + position, Qwen2KvPageMasks.cs:37, in 32-bit
+    // wrap-around), so each layer gets its own region.
+    const bool random = activation.selection == SYNAPSE_KV_SELECT_RANDOM;
+    const uint32_t list_layers = random ? dims.layers : 1;
+    std::vector<int32_t> lists(static_cast<size_t>(list_entries) * (list_entries > 0 ? list_layers : 0), -1);
+    std::vector<SelectJob> select_jobs;
+    std::vector<int32_t> drawn;
+    for (const Row& row : rows) {
+        if (row.list < 0) {
+            continue;
+        }
+        const Unit& unit = units[row.token];
+        const int32_t budget = static_cast<int32_t>(activation.budget_pages);
+        const int32_t position = tokens[row.token].position;
+        for (uint32_t layer = 0; layer < list_layers; ++layer) {
+            int32_t* list = &lists[static_cast<size_t>(layer) * list_entries + row.list];
+            list[0] = 0;
+            for (int32_t page = unit.window_page; page <= position / kStepKeys; ++page) {
+                list[1 + budget + page - unit.window_page] = page;
+            }
+            if (random) {
+                // RandomPages (KvPageSelector.cs:118-129): a partial Fisher-Yates draw over pages 1..candidates.
+                const uint32_t seed = static_cast<uint32_t>(activation.seed) * 1000003u + layer * 7919u +
+                                      static_cast<uint32_t>(row.kv_head) * 104729u + static_cast<uint32_t>(position);
+                SeededRandom generator(static_cast<int32_t>(seed));
+                drawn.resize(unit.candidates);
+                for (int32_t page = 0; page < unit.candidates; ++page) {
+                    drawn[page] = page + 1;
+                }
+                for (int32_t index = 0; index < budget; ++index) {
+                    std::swap(drawn[index], drawn[generator.next(index, unit.candidates)]);
+                }
+                std::sort(drawn.begin(), drawn.begin() + budget);
+                std::copy(drawn.begin(), drawn.begin() + budget, list + 1);
+            }
+        }
+        if (!random) {
+            select_jobs.push_back(SelectJob{row.token, row.kv_head, row.list, unit.candidates});
+        }
+    }
+
+    // Blocks the step writes (after copy-on-write), whose summaries each layer's append recomputes.
+    std::vector<int32_t> touched;
+    if (activation.enabled != 0) {
+        std::vector<int64_t> keys;
+        for (int32_t index = 0; index < count; ++index) {
+            const uint32_t position = static_cast<uint32_t>(tokens[index].position);
+            const int32_t page = cache.table[static_cast<size_t>(tokens[index].slot) * dims.pages_per_slot +
+                                             position / dims.page_tokens];
+            keys.push_back(static_cast<int64_t>(page) * 65536 + (position % dims.page_tokens) / kStepKeys);
+        }
+        std::sort(keys.begin(), keys.end());
+        keys.erase(std::unique(keys.begin(), keys.end()), keys.end());
+        for (int64_t key : keys) {
+            touched.push_back(static_cast<int32_t>(key / 65536));
+            touched.push_back(static_cast<int32_t>(key % 65536));
         }
     }
 
@@ -562,7 +763,8 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
                 const int32_t key_begin = row.key_begin + static_cast<int32_t>((step - row.first_step) * kStepKeys);
                 const int32_t key_end =
                     std::min<int32_t>(row.keys, row.key_begin + static_cast<int32_t>((stop - row.first_step) * kStepKeys));
-                segments.push_back(DecodeSegment{row.token, row.kv_head, key_begin, key_end, -1, -1, {0, 0}});
+                segments.push_back(DecodeSegment{row.token, row.kv_head, key_begin, key_end, -1, -1, row.list,
+                                                  stop == row_end ? 1 : 0});
                 step = stop;
             }
             row.pieces = static_cast<int32_t>(segments.size() - row.first_segment);
@@ -716,7 +918,10 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.segments_offset = align_up(cache.members_offset + members.size() * sizeof(int32_t), 256);
     cache.merges_offset = align_up(cache.segments_offset + segments.size() * sizeof(DecodeSegment), 256);
     cache.prefill_offset = align_up(cache.merges_offset + merges.size() * sizeof(MergeItem), 256);
-    const size_t total = cache.prefill_offset + prefill.size() * sizeof(PrefillItem);
+    cache.lists_offset = align_up(cache.prefill_offset + prefill.size() * sizeof(PrefillItem), 256);
+    cache.select_offset = align_up(cache.lists_offset + lists.size() * sizeof(int32_t), 256);
+    cache.touched_offset = align_up(cache.select_offset + select_jobs.size() * sizeof(SelectJob), 256);
+    const size_t total = cache.touched_offset + touched.size() * sizeof(int32_t);
     cache.blob.ensure(total, "step buffer");
     cache.partial_out.ensure(static_cast<size_t>(partial_rows) * group * dims.head_dim, "attention partials");
     cache.partial_ml.ensure(static_cast<size_t>(partial_rows) * group * 2, "attention partial statistics");
@@ -727,6 +932,9 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     std::memcpy(staging + cache.segments_offset, segments.data(), segments.size() * sizeof(DecodeSegment));
     std::memcpy(staging + cache.merges_offset, merges.data(), merges.size() * sizeof(MergeItem));
     std::memcpy(staging + cache.prefill_offset, prefill.data(), prefill.size() * sizeof(PrefillItem));
+    std::memcpy(staging + cache.lists_offset, lists.data(), lists.size() * sizeof(int32_t));
+    std::memcpy(staging + cache.select_offset, select_jobs.data(), select_jobs.size() * sizeof(SelectJob));
+    std::memcpy(staging + cache.touched_offset, touched.data(), touched.size() * sizeof(int32_t));
     cache.uploader.copy(cache.blob.pointer, total, cache.stream);
     cache.step_count = count;
     cache.decode_workers = workers;
@@ -735,16 +943,21 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.prefill_items = prompt_items;
     cache.listed_items = static_cast<int32_t>(listed.size());
     cache.listed_tiles = listed_tiles;
+    cache.list_layer_entries = random ? static_cast<size_t>(list_entries) : 0;
+    cache.select_jobs = static_cast<int32_t>(select_jobs.size());
+    cache.touched_blocks = static_cast<int32_t>(touched.size() / 2);
     // The fused append + decode launch needs every token to own its slot (no token may read another token's
     // position of the same step, and each (token, KV head) row appends its own position only) and no prompt run
     // (whose K/V must be in the pages before its attention); listed items read only pages below every member's
-    // position.
+    // position. Under KV page activation every append goes first (its blocks' summaries are recomputed before the
+    // selection reads them).
     std::vector<int32_t> slots(count);
     for (int32_t index = 0; index < count; ++index) {
         slots[index] = tokens[index].slot;
     }
     std::sort(slots.begin(), slots.end());
-    cache.fusable = prompt_items == 0 && std::adjacent_find(slots.begin(), slots.end()) == slots.end();
+    cache.fusable = prompt_items == 0 && std::adjacent_find(slots.begin(), slots.end()) == slots.end() &&
+                    activation.enabled == 0;
     cache.step_ready = true;
 }
 
@@ -946,6 +1159,19 @@ void launch_append_layer(SynapseKvCache& cache, uint32_t layer, float* qkv, uint
     check_hip(launch_append(launch_for(cache, SYNAPSE_KV_KERNEL_APPEND, cache.step_count > 0), args, cache.step_count,
                             dims.precision == SYNAPSE_KV_F16),
               "append");
+    if (cache.activation.enabled != 0) {
+        SummaryArgs summary{};
+        summary.geo = args.geo;
+        summary.summaries = cache.summaries.pointer;
+        summary.summary_page_bytes = cache.summary_page_bytes;
+        summary.blocks = reinterpret_cast<const int32_t*>(cache.blob.pointer + cache.touched_offset);
+        summary.count = cache.touched_blocks;
+        summary.first_layer = static_cast<int32_t>(layer);
+        summary.layers = 1;
+        check_hip(launch_summaries(launch_for(cache, SYNAPSE_KV_KERNEL_PAGE_SELECT, summary.count > 0), summary,
+                                   dims.precision == SYNAPSE_KV_F16),
+                  "key summaries");
+    }
 }
 
 // Attention of the prepared step for one layer; with `append`, the step's K/V are appended first (fused into the
@@ -992,7 +1218,27 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
     args.prefill = reinterpret_cast<const PrefillItem*>(cache.blob.pointer + cache.prefill_offset);
     args.partial_out = cache.partial_out.pointer;
     args.partial_ml = cache.partial_ml.pointer;
+    int32_t* lists = reinterpret_cast<int32_t*>(cache.blob.pointer + cache.lists_offset) +
+                     static_cast<size_t>(layer) * cache.list_layer_entries;
+    args.lists = lists;
     const bool fp16 = dims.precision == SYNAPSE_KV_F16;
+    if (cache.select_jobs > 0) {
+        SelectArgs select{};
+        select.geo = args.geo;
+        select.tokens = args.tokens;
+        select.qkv = qkv;
+        select.qkv_stride = static_cast<int32_t>(qkv_stride);
+        select.rotate = args.rotate;
+        select.cosines = cache.cosines.pointer;
+        select.sines = cache.sines.pointer;
+        select.summaries = cache.summaries.pointer;
+        select.summary_page_bytes = cache.summary_page_bytes;
+        select.jobs = reinterpret_cast<const SelectJob*>(cache.blob.pointer + cache.select_offset);
+        select.lists = lists;
+        select.budget = static_cast<int32_t>(cache.activation.budget_pages);
+        check_hip(launch_select(launch_for(cache, SYNAPSE_KV_KERNEL_PAGE_SELECT, true), select, cache.select_jobs, fp16),
+                  "page selection");
+    }
     const int prompt_items = cache.prefill_items;
     const int listed_items = cache.listed_items;
     if (cache.listed_tiles == 1) {
@@ -1209,7 +1455,8 @@ int32_t synapse_kv_fork(SynapseKvCache* cache, uint32_t source, uint32_t target)
     });
 }
 
-int32_t synapse_kv_step(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count) {
+int32_t synapse_kv_step_prompt(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count,
+                               size_t prompt_start) {
     if (cache == nullptr || tokens == nullptr) {
         return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or tokens");
     }
@@ -1217,11 +1464,86 @@ int32_t synapse_kv_step(SynapseKvCache* cache, const SynapseKvBatchToken* tokens
         if (count == 0 || count > cache->dims.step_tokens) {
             invalid("a step holds 1.." + std::to_string(cache->dims.step_tokens) + " tokens");
         }
+        if (prompt_start > count) {
+            invalid("prompt_start is past the step's last token");
+        }
         set_device(*cache);
         cache->step_ready = false;
         prepare_step(*cache, tokens, static_cast<int32_t>(count));
         flush_ops(*cache);
+        cache->prompt_start = static_cast<int32_t>(prompt_start);
         plan_step(*cache, tokens, static_cast<int32_t>(count));
+    });
+}
+
+int32_t synapse_kv_step(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count) {
+    return synapse_kv_step_prompt(cache, tokens, count, count);
+}
+
+int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPageActivation* activation) {
+    if (cache == nullptr || activation == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache or activation");
+    }
+    return guarded([&] {
+        const SynapseKvPageActivation wanted = *activation;
+        if (wanted.enabled != 0) {
+            // KvPageActivation.Validate (KvPageActivation.cs:23-37); 16- and 32-position pages are not built here.
+            if (wanted.page_tokens == 16 || wanted.page_tokens == 32) {
+                fail(SYNAPSE_KV_UNAVAILABLE, "KV page activation selects 64-position pages here (" +
+                                                 std::to_string(wanted.page_tokens) + " requested)");
+            }
+            if (wanted.page_tokens != 64) {
+                invalid("KV pages hold 16, 32, or 64 positions");
+            }
+            if (wanted.selection != SYNAPSE_KV_SELECT_KEY_BOUND && wanted.selection != SYNAPSE_KV_SELECT_RANDOM) {
+                invalid("unknown KV page selection " + std::to_string(wanted.selection));
+            }
+            if (wanted.budget_pages > INT32_MAX || wanted.window_tokens > INT32_MAX) {
+                invalid("budget_pages and window_tokens must be non-negative 32-bit integers");
+            }
+        }
+        set_device(*cache);
+        cache->step_ready = false;
+        const bool rebuild = wanted.enabled != 0 && cache->activation.enabled == 0;
+        if (wanted.enabled != 0 && cache->summaries.pointer == nullptr) {
+            const Dims& dims = cache->dims;
+            cache->summary_page_bytes =
+                summary_page_elements(dims.layers, dims.kv_heads, dims.page_tokens, dims.head_dim) *
+                (dims.precision == SYNAPSE_KV_F16 ? 2 : 4);
+            cache->summaries.ensure(cache->summary_page_bytes * dims.max_pages, "key summaries");
+        }
+        if (rebuild) {
+            // Summaries of every block of every mapped page, all layers.
+            const Dims& dims = cache->dims;
+            std::vector<int32_t> blocks;
+            for (uint32_t page = 0; page < dims.max_pages; ++page) {
+                if (cache->refcount[page] > 0) {
+                    for (uint32_t block = 0; block < dims.page_tokens / kStepKeys; ++block) {
+                        blocks.push_back(static_cast<int32_t>(page));
+                        blocks.push_back(static_cast<int32_t>(block));
+                    }
+                }
+            }
+            if (!blocks.empty()) {
+                const size_t bytes = blocks.size() * sizeof(int32_t);
+                cache->op_blob.ensure(bytes, "operation buffer");
+                void* staging = cache->uploader.acquire(bytes);
+                std::memcpy(staging, blocks.data(), bytes);
+                cache->uploader.copy(cache->op_blob.pointer, bytes, cache->stream);
+                SummaryArgs summary{};
+                summary.geo = geometry(*cache, 0);
+                summary.summaries = cache->summaries.pointer;
+                summary.summary_page_bytes = cache->summary_page_bytes;
+                summary.blocks = reinterpret_cast<const int32_t*>(cache->op_blob.pointer);
+                summary.count = static_cast<int32_t>(blocks.size() / 2);
+                summary.first_layer = 0;
+                summary.layers = static_cast<int32_t>(dims.layers);
+                check_hip(launch_summaries(launch_for(*cache, SYNAPSE_KV_KERNEL_PAGE_SELECT, true), summary,
+                                           dims.precision == SYNAPSE_KV_F16),
+                          "key summaries");
+            }
+        }
+        cache->activation = wanted;
     });
 }
 

@@ -54,7 +54,9 @@ struct PageArgs {
 };
 
 // A decode segment: keys [key_begin, key_end) of one (token, KV head) row. `row` >= 0 is the segment's partial
-// row and `merge` the row's merge entry; row -1 writes the normalized output directly.
+// row and `merge` the row's merge entry; row -1 writes the normalized output directly. With list >= 0 the row
+// attends the 64-key blocks lists[list + 0 ..] (KV page activation) and key_begin / key_end count list entries
+// times 64. `last` marks the piece that holds the row's own position (the fused append writes it first).
 struct DecodeSegment {
     int32_t token;
     int32_t kv_head;
@@ -62,7 +64,8 @@ struct DecodeSegment {
     int32_t key_end;
     int32_t row;
     int32_t merge;
-    int32_t pad[2];
+    int32_t list;
+    int32_t last;
 };
 static_assert(sizeof(DecodeSegment) == 32, "DecodeSegment is 32 bytes");
 
@@ -136,6 +139,7 @@ struct AttentionArgs {
     const int32_t* worker_segments;  // [workers + 1]: worker w walks segments [ws[w], ws[w + 1])
     const DecodeSegment* segments;
     const int32_t* members;  // step token indices of listed prefill items' columns
+    const int32_t* lists;    // block lists of rows under KV page activation (DecodeSegment::list)
     const MergeItem* merges;
     const PrefillItem* prefill;
     float* partial_out;  // [rows][group][head_dim]
@@ -182,6 +186,53 @@ struct ProjectionArgs {
     int64_t partial_stride;  // total_tiles * 16
 };
 
+// KV page activation (ADR-016). Key summaries live in their own buffer, one summary page per pool page:
+// [layer][kv_head][64-key block of the page][min, max][head_dim] in the storage type (exact minima and maxima of the
+// stored keys).
+inline uint64_t summary_page_elements(int layers, int kv_heads, int page_tokens, int head_dim) {
+    return static_cast<uint64_t>(layers) * kv_heads * (page_tokens / 64) * 2 * head_dim;
+}
+
+// Recomputes the summaries of `count` (pool page, 64-key block of the page) pairs for layers
+// [first_layer, first_layer + layers) from the stored keys.
+struct SummaryArgs {
+    Geometry geo;  // geo.layer unused
+    uint8_t* summaries;
+    uint64_t summary_page_bytes;
+    const int32_t* blocks;  // (page, block) pairs
+    int32_t count;
+    int32_t first_layer;
+    int32_t layers;
+    int32_t pad;
+};
+
+// One key-bound selection: the row (token, kv_head) ranks blocks 1..candidates of its slot and writes the `budget`
+// best (ascending) to lists[list + 1 ..] (lists[list] is the sink block, the window blocks follow the budget).
+constexpr int kMaxSelectCandidates = 4096;  // blocks one key-bound selection ranks (262,144 positions)
+struct SelectJob {
+    int32_t token;
+    int32_t kv_head;
+    int32_t list;
+    int32_t candidates;
+};
+static_assert(sizeof(SelectJob) == 16, "SelectJob is 16 bytes");
+
+struct SelectArgs {
+    Geometry geo;
+    const SynapseKvBatchToken* tokens;
+    const float* qkv;
+    int32_t qkv_stride;
+    int32_t rotate;  // 1: Q in qkv is unrotated (append_attention); the bound uses the rotated query
+    const float* cosines;
+    const float* sines;
+    const uint8_t* summaries;
+    uint64_t summary_page_bytes;
+    const SelectJob* jobs;
+    int32_t* lists;
+    int32_t budget;
+    int32_t pad;
+};
+
 // Page regions are stored in MFMA-fragment order; see page_layout.h.
 
 // Where a kernel goes: the cache's stream, and (when profiling) the events its dispatch records at start and end.
@@ -209,6 +260,8 @@ int prefill_resident_blocks(int device, int head_dim, int group);
 // Prefill items [first, first + items) with `tiles` (1 or kPrefillTiles) column tiles of 16 tokens per wave.
 hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int first, int items, int tiles, bool fp16);
 hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16);
+hipError_t launch_summaries(const Launch& launch, const SummaryArgs& args, bool fp16);
+hipError_t launch_select(const Launch& launch, const SelectArgs& args, int jobs, bool fp16);
 // A projection over `tiles` row tiles (all segments); token tiles of 16 * projection_token_tiles(tokens).
 hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles);
 int projection_token_tiles(int tokens);

@@ -11,6 +11,11 @@ and error behaviour:
 * ``allocated_bytes`` -- ``AllocatedKvBytes`` / ``synapse_gpu_decoder_kv_bytes`` (ffi.rs:229-248);
 * ``step`` + ``append_rope`` + ``attention`` -- one layer of ``IBatchDecoder.Forward``'s attention half
   (step/layers.rs:62-148, step/attention.rs:9-145) for a batch of ``BatchToken`` (decoder.rs:133-141);
+* ``step(tokens, prompt_start)`` -- ``Forward(tokens, promptStart)``: tokens from ``prompt_start`` on are prompt
+  tokens;
+* ``set_page_activation(budget_pages, window_tokens, ...)`` -- ``ModelLoadOptions.KvPageActivation`` (ADR-016,
+  KvPageActivation.cs, KvPageSelector.cs, Qwen2KvPageMasks.cs): decode units attend the sink page, the recent
+  window and the budgeted pages;
 * ``fork`` / ``truncate`` -- prefix reuse (DirectSessionPrefix.cs:16-41) as copy-on-write page sharing, and
   rollback (native/synapse-core/src/Features/SessionState/kv_pages.rs:158-177).
 
@@ -30,7 +35,10 @@ from .native import (
     OPTION_PREFILL_RUNS,
     OPTION_PREFILL_SPLIT_KEYS,
     OPTION_SPLIT_KEYS,
+    SELECT_KEY_BOUND,
+    SELECT_RANDOM,
     BatchToken,
+    PageActivation,
     CacheDesc,
     NativeKvLibrary,
     KERNEL_KINDS,
@@ -219,9 +227,33 @@ class PagedKvCache:
         return {"capacity": capacity.value, "length": length.value, "pages": pages.value}
 
     # -- the step ------------------------------------------------------------------------------------------
-    def step(self, tokens) -> None:
+    def step(self, tokens, prompt_start: int | None = None) -> None:
+        """Prepares a step; tokens from ``prompt_start`` on (default: none) are prompt tokens."""
         buffer = tokens if isinstance(tokens, ctypes.Array) else batch_tokens(tokens)
-        self.library.check(self.library.c_step(self.handle, buffer, len(buffer)))
+        if prompt_start is None:
+            self.library.check(self.library.c_step(self.handle, buffer, len(buffer)))
+        else:
+            if prompt_start < 0:
+                raise ValueError("prompt_start must be non-negative")
+            self.library.check(self.library.c_step_prompt(self.handle, buffer, len(buffer), prompt_start))
+
+    def set_page_activation(self, budget_pages: int | None, window_tokens: int = 0, page_tokens: int = 64,
+                            selection: str = "key_bound", seed: int = 0) -> None:
+        """KV page activation (``KvPageActivation(BudgetPages, WindowTokens)``); ``None`` restores dense attention.
+
+        ``selection`` is ``"key_bound"`` (KvPageSelection.KeyBound) or ``"random"`` (the control). Negative budgets
+        or windows raise ValueError (ArgumentOutOfRangeException in KvPageActivation.Validate).
+        """
+        if budget_pages is None:
+            activation = PageActivation(0, 0, 0, 64, SELECT_KEY_BOUND, 0)
+        else:
+            if budget_pages < 0 or window_tokens < 0:
+                raise ValueError("budget_pages and window_tokens must be non-negative")
+            kinds = {"key_bound": SELECT_KEY_BOUND, "random": SELECT_RANDOM}
+            if selection not in kinds:
+                raise ValueError(f"unknown KV page selection {selection!r}")
+            activation = PageActivation(1, budget_pages, window_tokens, page_tokens, kinds[selection], seed)
+        self.library.check(self.library.c_set_page_activation(self.handle, ctypes.byref(activation)))
 
     def append_rope(self, layer: int, qkv, qkv_stride: int | None = None) -> None:
         stride = self.qkv_width if qkv_stride is None else qkv_stride

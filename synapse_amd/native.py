@@ -16,7 +16,7 @@ import ctypes
 import threading
 from pathlib import Path
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libsynapse_kv.so"
 
 STATUS_OK = 0
@@ -36,6 +36,9 @@ OPTION_PREFILL_SPLIT_KEYS = 3
 OPTION_DECODE_PREFETCH = 4
 OPTION_PROFILE_EVERY = 5
 OPTION_SHARED_PREFIX = 6
+
+SELECT_KEY_BOUND = 0
+SELECT_RANDOM = 1
 
 
 class SynapseKvError(RuntimeError):
@@ -111,7 +114,7 @@ class PageStats(ctypes.Structure):
     ]
 
 
-KERNEL_KINDS = ("table", "pages", "append", "decode", "merge", "prefill", "gather")
+KERNEL_KINDS = ("table", "pages", "append", "decode", "merge", "prefill", "gather", "page_select")
 
 NO_BIAS = (1 << 64) - 1
 
@@ -142,13 +145,26 @@ class Projection(ctypes.Structure):
     ]
 
 
+class PageActivation(ctypes.Structure):
+    """SynapseKvPageActivation: KvPageActivation (KvPageActivation.cs:10-37) plus an enable flag."""
+
+    _fields_ = [
+        ("enabled", ctypes.c_uint32),
+        ("budget_pages", ctypes.c_uint32),
+        ("window_tokens", ctypes.c_uint32),
+        ("page_tokens", ctypes.c_uint32),
+        ("selection", ctypes.c_uint32),
+        ("seed", ctypes.c_int32),
+    ]
+
+
 class Profile(ctypes.Structure):
     _fields_ = [("launches", ctypes.c_uint64 * 8), ("milliseconds", ctypes.c_double * 8)]
 
 
 # Sizes pinned on both sides of the ABI (include/synapse_kv.h static assertions).
 STRUCT_SIZES = {DeviceInfo: 152, BatchToken: 16, CacheDesc: 64, PageStats: 40, Profile: 128, Matrix: 24,
-                Projection: 48}
+                Projection: 48, PageActivation: 24}
 for _struct, _size in STRUCT_SIZES.items():
     assert ctypes.sizeof(_struct) == _size, (_struct.__name__, ctypes.sizeof(_struct))
 
@@ -173,6 +189,8 @@ EXPORTS = {
     "synapse_kv_truncate": (_I32, [_P, _U32, _U32]),
     "synapse_kv_fork": (_I32, [_P, _U32, _U32]),
     "synapse_kv_step": (_I32, [_P, ctypes.POINTER(BatchToken), _SIZE]),
+    "synapse_kv_step_prompt": (_I32, [_P, ctypes.POINTER(BatchToken), _SIZE, _SIZE]),
+    "synapse_kv_set_page_activation": (_I32, [_P, ctypes.POINTER(PageActivation)]),
     "synapse_kv_append_rope": (_I32, [_P, _U32, _P, _U32]),
     "synapse_kv_attention": (_I32, [_P, _U32, _P, _U32, _P, _U32]),
     "synapse_kv_append_attention": (_I32, [_P, _U32, _P, _U32, _P, _U32]),

@@ -48,6 +48,10 @@ SIGNATURES = {
     "orc_attention_fp64": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
     "orc_attention_split": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "orc_paged_attention": (ctypes.c_double, [_P, _I, _P, _I, _P, _I, _I]),
+    "orc_paged_attention_pages": (ctypes.c_double, [_P, _I, _P, _I, _P, _I, _I, _P, _I, _P]),
+    "orc_dotnet_random": (None, [ctypes.c_int32, _I, ctypes.c_int32, ctypes.c_int32, _P]),
+    "orc_page_bound": (_F, [_P, _I, _I, _P, _I, _I]),
+    "orc_page_select": (None, [_I, _I, _I, _I, _P, _I, _I, _P, _I, ctypes.c_int32, _P]),
     "orc_plan_attention": (_I, [_P, _I, _I, _I, _P, _I, _P]),
     "orc_prefix_create": (_P, [_I]),
     "orc_prefix_destroy": (None, [_P]),
@@ -241,9 +245,19 @@ class PagedCache:
     def kv_bytes(self):
         return ORACLE.orc_paged_kv_bytes(self.handle)
 
-    def attention(self, layer, qkv, out, threads=1):
-        return ORACLE.orc_paged_attention(self.handle, layer, ptr(qkv), qkv.shape[1], ptr(out), out.shape[1],
-                                          threads)
+    def attention(self, layer, qkv, out, threads=1, activation=None, prompt_start=None, maximum=None):
+        """Step attention for one layer. With ``activation`` = (budget, window, page_tokens, selection, seed) the
+        decode units attend their selected pages; then returns the masks [tokens][kv_heads][maximum] (bool)."""
+        if activation is None:
+            return ORACLE.orc_paged_attention(self.handle, layer, ptr(qkv), qkv.shape[1], ptr(out), out.shape[1],
+                                              threads)
+        parameters = np.asarray(activation, dtype=np.int32)
+        tokens = qkv.shape[0]
+        start = tokens if prompt_start is None else prompt_start
+        masks = np.zeros((tokens, self.kv_heads, maximum), dtype=np.uint8)
+        ORACLE.orc_paged_attention_pages(self.handle, layer, ptr(qkv), qkv.shape[1], ptr(out), out.shape[1], threads,
+                                         ptr(parameters), start, ptr(masks))
+        return masks.astype(bool)
 
 
 def plan_attention(tokens, kv_heads, run_tokens):
@@ -301,3 +315,26 @@ def q8_project(segments, inputs, output, accumulate=False, exact=False, threads=
         return magnitude
     return ORACLE.orc_q8_project_f32(weights, bias_pointers, rows, out_columns, count, columns, tokens, ptr(inputs),
                                      inputs.shape[1], ptr(output), output.shape[1], int(accumulate), threads)
+
+
+def dotnet_random(seed, count, low=0, high=0):
+    """System.Random(seed): Next() (low == high == 0) or Next(low, high), ``count`` times."""
+    out = np.zeros(count, dtype=np.int32)
+    ORACLE.orc_dotnet_random(seed, count, low, high, ptr(out))
+    return out
+
+
+def page_bound(queries, group, head_dim, keys, first, last):
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    k = np.ascontiguousarray(keys, dtype=np.float32)
+    return float(ORACLE.orc_page_bound(ptr(q), group, head_dim, ptr(k), first, last))
+
+
+def page_select(budget, window, queries, group, head_dim, keys, position, seed=0, page_tokens=64, random=False):
+    """KvPageSelector.Select: the selected positions 0..position (bool)."""
+    q = np.ascontiguousarray(queries, dtype=np.float32)
+    k = np.ascontiguousarray(keys, dtype=np.float32)
+    selected = np.zeros(position + 1, dtype=np.uint8)
+    ORACLE.orc_page_select(budget, window, page_tokens, 1 if random else 0, ptr(q), group, head_dim, ptr(k), position,
+                           seed, ptr(selected))
+    return selected.astype(bool)

@@ -41,7 +41,7 @@ def test_header_compiles_with_pinned_sizes(compiler, flag, tmp_path):
 def test_abi_version_and_struct_sizes(native):
     from synapse_amd.native import ABI_VERSION, STRUCT_SIZES
 
-    assert native.c_abi_version() == ABI_VERSION == 2
+    assert native.c_abi_version() == ABI_VERSION == 3
     for struct, size in STRUCT_SIZES.items():
         assert ctypes.sizeof(struct) == size
 
