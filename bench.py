@@ -69,6 +69,30 @@ def prefill(cache, torch, lengths, generator, chunk=4096):
     torch.cuda.synchronize()
 
 
+def parse_kv_pages(text: str | None) -> dict | None:
+    """--kv-pages <budget>:<window>[:random[:seed]] (the reference CLI's option, ADR-016)."""
+    if text is None:
+        return None
+    parts = text.split(":")
+    if len(parts) < 2 or len(parts) > 4 or (len(parts) > 2 and parts[2] != "random"):
+        sys.exit("--kv-pages takes <budget>:<window>[:random[:seed]]")
+    budget, window = int(parts[0]), int(parts[1])
+    random = len(parts) > 2
+    seed = int(parts[3]) if len(parts) > 3 else 0
+    name = f"kvpages{budget}w{window}" + ("r" if random else "")
+    return {"budget": budget, "window": window, "selection": "random" if random else "key_bound", "seed": seed,
+            "name": name}
+
+
+def attended_keys(position: int, activation: dict) -> int:
+    """Positions a decode token at `position` attends (KvPageSelector.Select with 64-position pages)."""
+    count = position + 1
+    window_page = max(0, count - activation["window"]) // 64
+    if max(0, window_page - 1) <= activation["budget"]:
+        return count
+    return 64 + activation["budget"] * 64 + (count - window_page * 64)
+
+
 def cpu_baseline(lengths, threads: int) -> dict:
     """The reference CPU attention restated in C++ (oracle/), timed on host threads: one layer of one decode step
     over the same lengths (FP16 pages widened exactly, Qwen2CpuAttention order), extrapolated to 28 layers."""
@@ -559,6 +583,8 @@ def main() -> None:
     parser.add_argument("--separate", action="store_true",
                         help="append_rope + attention as two launches instead of the fused append_attention")
     parser.add_argument("--cpu-threads", type=int, default=None)
+    parser.add_argument("--kv-pages", default=None, metavar="BUDGET:WINDOW[:random[:SEED]]",
+                        help="c3 under query-aware KV page activation (the reference CLI's --kv-pages)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -590,6 +616,7 @@ def main() -> None:
     stream = torch.cuda.current_stream()
     cache.set_stream(stream)
     apply_options(args, cache)
+    activation = parse_kv_pages(args.kv_pages)
     for slot, length in enumerate(lengths.tolist()):
         cache.reserve(slot, length + total_steps + 1)
     generator = torch.Generator(device="cuda")
@@ -597,6 +624,9 @@ def main() -> None:
     started = time.perf_counter()
     prefill(cache, torch, lengths, generator)
     log(f"prefill {time.perf_counter() - started:.1f} s; KV bytes {cache.allocated_bytes / 2**30:.2f} GiB")
+    if activation is not None:
+        cache.set_page_activation(activation["budget"], activation["window"], selection=activation["selection"],
+                                  seed=activation["seed"])
 
     width = (HEADS + 2 * KV_HEADS) * HEAD_DIM
     qkv = torch.empty((LAYERS, SEQUENCES, width), device="cuda").normal_(generator=generator)
@@ -635,6 +665,10 @@ def main() -> None:
     # Algorithmic bytes: each step reads the K/V of every attended position once per layer and writes the new
     # token's K/V; q/out rows are read/written once (fp32).
     keys_per_step = [int((lengths + args.warmup + index + 1).sum()) for index in range(args.steps)]
+    dense_keys_per_step = keys_per_step
+    if activation is not None:
+        keys_per_step = [sum(attended_keys(int(n) + args.warmup + index, activation) for n in lengths)
+                         for index in range(args.steps)]
     q_bytes = SEQUENCES * HEADS * HEAD_DIM * 4
     kv_row_bytes = SEQUENCES * 2 * KV_HEADS * HEAD_DIM * 4  # the new token's fp32 K and V rows
     append_bytes = SEQUENCES * KV_BYTES_PER_TOKEN_LAYER  # the new token's FP16 K and V
@@ -650,7 +684,7 @@ def main() -> None:
     traffic = measured_traffic()
 
     result = {
-        "metric": METRIC,
+        "metric": METRIC if activation is None else METRIC + ", KV page activation " + activation["name"],
         "value": round(tokens_per_second, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -669,6 +703,11 @@ def main() -> None:
             "layers": LAYERS, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM, "sequences": SEQUENCES,
             "page_tokens": PAGE_TOKENS, "lengths": lengths.tolist(), "parallelism": "single GPU",
         },
+        **({} if activation is None else {"kv_pages": {
+            **activation, "attended_keys_per_step": int(statistics.mean(keys_per_step)),
+            "dense_keys_per_step": int(statistics.mean(dense_keys_per_step)),
+            "page_select_us_per_layer": round(kernels["page_select"][1] * 1e3 / kernels["page_select"][0], 2)
+            if "page_select" in kernels else None}}),
         "hbm_gbps": round(step_gbps, 1),
         "host_ms_per_step": round(host_seconds * 1e3 / args.steps, 4),
         "hbm_frac_of_peak": round(step_gbps / PEAK_HBM_GBPS, 4),
@@ -688,7 +727,7 @@ def main() -> None:
             "kernels_ms": {kind: round(ms, 3) for kind, (count, ms) in kernels.items()},
         },
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and activation is None:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         log(f"cpu baseline on {threads} threads")
         baseline = cpu_baseline(lengths, threads)

@@ -102,12 +102,12 @@ typedef struct SynapseKvPageStats {
 /* GPU time per kernel kind between synapse_kv_profile_begin and _end, 128 bytes. */
 #define SYNAPSE_KV_KERNEL_TABLE 0   /* block-table operations */
 #define SYNAPSE_KV_KERNEL_PAGES 1   /* page zero-fill and copy-on-write copies */
-#define SYNAPSE_KV_KERNEL_APPEND 2  /* RoPE + KV append */
+#define SYNAPSE_KV_KERNEL_APPEND 2  /* RoPE + KV append (and key summaries under KV page activation) */
 #define SYNAPSE_KV_KERNEL_DECODE 3  /* split-K decode attention (with the fused append when used) */
 #define SYNAPSE_KV_KERNEL_MERGE 4   /* split merge */
 #define SYNAPSE_KV_KERNEL_PREFILL 5 /* prompt-run attention, and shared-prefix pages read once for their sharers */
 #define SYNAPSE_KV_KERNEL_GATHER 6  /* KV read-back */
-#define SYNAPSE_KV_KERNEL_PAGE_SELECT 7 /* KV page activation: key summaries and page selection */
+#define SYNAPSE_KV_KERNEL_PAGE_SELECT 7 /* KV page activation: key-bound page selection */
 typedef struct SynapseKvProfile {
     uint64_t launches[8];
     double milliseconds[8];

@@ -274,8 +274,12 @@ struct SynapseKvCache {
     size_t list_layer_entries = 0;   // entries per layer in the blob (random lists differ per layer), else 0
     size_t select_offset = 0;        // key-bound selection jobs
     int32_t select_jobs = 0;
-    size_t touched_offset = 0;       // (page, block) pairs the step writes: summaries recomputed after appends
+    size_t touched_offset = 0;       // (page, block) pairs the step writes: their summaries follow each append
     int32_t touched_blocks = 0;
+    bool select_reads_touched = false;  // a selection ranks a block the step writes (window 0 at a block's end)
+    int32_t most_candidates = 0;     // largest key-bound selection job
+    synapse_kv::DeviceBuffer<uint64_t> select_keys;
+    synapse_kv::DeviceBuffer<int32_t> select_counters;  // zeroed when allocated; the select kernel leaves them 0
 
     ~SynapseKvCache() {
         (void)hipSetDevice(device);
@@ -298,6 +302,8 @@ struct SynapseKvCache {
         partial_out.reset();
         partial_ml.reset();
         summaries.reset();
+        select_keys.reset();
+        select_counters.reset();
         if (pool != nullptr) {
             (void)hipFree(pool);
         }
@@ -494,6 +500,12 @@ int64_t choose_prefill_chunk(const SynapseKvCache& cache, const SynapseKvBatchTo
     return best_chunk;
 }
 
+// Rank keys one key-bound selection job keeps between its tiles and its last tile.
+size_t select_key_stride(const SynapseKvCache& cache, int32_t most_candidates) {
+    const size_t tiles = (static_cast<size_t>(most_candidates) + 63) / 64;
+    return tiles * std::min<size_t>(cache.activation.budget_pages, 64);
+}
+
 // Builds and uploads the attention plan of a prepared step.
 //
 // Lone tokens (and prompt runs of FP32 caches) go to the decode kernel: every (token, KV head) row is cut into
@@ -666,6 +678,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     const uint32_t list_layers = random ? dims.layers : 1;
     std::vector<int32_t> lists(static_cast<size_t>(list_entries) * (list_entries > 0 ? list_layers : 0), -1);
     std::vector<SelectJob> select_jobs;
+    int32_t most_candidates = 0;
     std::vector<int32_t> drawn;
     for (const Row& row : rows) {
         if (row.list < 0) {
@@ -698,18 +711,26 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         }
         if (!random) {
             select_jobs.push_back(SelectJob{row.token, row.kv_head, row.list, unit.candidates});
+            most_candidates = std::max(most_candidates, unit.candidates);
         }
     }
 
-    // Blocks the step writes (after copy-on-write), whose summaries each layer's append recomputes.
+    // Blocks the step writes (after copy-on-write), whose summaries each layer recomputes after its appends. A
+    // decode unit's candidates end below its window, so the step's own blocks are candidates only with no window
+    // at a block's last position; otherwise the summary work can ride along in the selection launch.
     std::vector<int32_t> touched;
+    bool select_reads_touched = false;
     if (activation.enabled != 0) {
-        std::vector<int64_t> keys;
+        std::vector<int64_t> keys;  // page * 65536 + block
         for (int32_t index = 0; index < count; ++index) {
             const uint32_t position = static_cast<uint32_t>(tokens[index].position);
             const int32_t page = cache.table[static_cast<size_t>(tokens[index].slot) * dims.pages_per_slot +
                                              position / dims.page_tokens];
             keys.push_back(static_cast<int64_t>(page) * 65536 + (position % dims.page_tokens) / kStepKeys);
+            const Unit& unit = units[index];
+            if (unit.window_page >= 0 && unit.window_page - 1 >= static_cast<int32_t>(position / kStepKeys)) {
+                select_reads_touched = true;
+            }
         }
         std::sort(keys.begin(), keys.end());
         keys.erase(std::unique(keys.begin(), keys.end()), keys.end());
@@ -922,6 +943,13 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.select_offset = align_up(cache.lists_offset + lists.size() * sizeof(int32_t), 256);
     cache.touched_offset = align_up(cache.select_offset + select_jobs.size() * sizeof(SelectJob), 256);
     const size_t total = cache.touched_offset + touched.size() * sizeof(int32_t);
+    cache.select_keys.ensure(select_jobs.size() * select_key_stride(cache, most_candidates), "page selection keys");
+    if (select_jobs.size() > cache.select_counters.count) {
+        cache.select_counters.ensure(std::max<size_t>(select_jobs.size(), 256), "page selection counters");
+        check_hip(hipMemsetAsync(cache.select_counters.pointer, 0, cache.select_counters.count * sizeof(int32_t),
+                                 cache.stream),
+                  "page selection counters");
+    }
     cache.blob.ensure(total, "step buffer");
     cache.partial_out.ensure(static_cast<size_t>(partial_rows) * group * dims.head_dim, "attention partials");
     cache.partial_ml.ensure(static_cast<size_t>(partial_rows) * group * 2, "attention partial statistics");
@@ -945,7 +973,9 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.listed_tiles = listed_tiles;
     cache.list_layer_entries = random ? static_cast<size_t>(list_entries) : 0;
     cache.select_jobs = static_cast<int32_t>(select_jobs.size());
+    cache.most_candidates = most_candidates;
     cache.touched_blocks = static_cast<int32_t>(touched.size() / 2);
+    cache.select_reads_touched = select_reads_touched;
     // The fused append + decode launch needs every token to own its slot (no token may read another token's
     // position of the same step, and each (token, KV head) row appends its own position only) and no prompt run
     // (whose K/V must be in the pages before its attention); listed items read only pages below every member's
@@ -1144,7 +1174,10 @@ void require_step(const SynapseKvCache& cache, uint32_t layer) {
     }
 }
 
-void launch_append_layer(SynapseKvCache& cache, uint32_t layer, float* qkv, uint32_t qkv_stride, bool write_back) {
+// The step's appends for one layer; under KV page activation the written blocks' summaries follow (a summary
+// launch) unless `defer_summaries` (the caller's selection launch carries them).
+void launch_append_layer(SynapseKvCache& cache, uint32_t layer, float* qkv, uint32_t qkv_stride, bool write_back,
+                         bool defer_summaries = false) {
     const Dims& dims = cache.dims;
     AppendArgs args{};
     args.geo = geometry(cache, layer);
@@ -1159,7 +1192,7 @@ void launch_append_layer(SynapseKvCache& cache, uint32_t layer, float* qkv, uint
     check_hip(launch_append(launch_for(cache, SYNAPSE_KV_KERNEL_APPEND, cache.step_count > 0), args, cache.step_count,
                             dims.precision == SYNAPSE_KV_F16),
               "append");
-    if (cache.activation.enabled != 0) {
+    if (cache.activation.enabled != 0 && cache.touched_blocks > 0 && !defer_summaries) {
         SummaryArgs summary{};
         summary.geo = args.geo;
         summary.summaries = cache.summaries.pointer;
@@ -1168,7 +1201,7 @@ void launch_append_layer(SynapseKvCache& cache, uint32_t layer, float* qkv, uint
         summary.count = cache.touched_blocks;
         summary.first_layer = static_cast<int32_t>(layer);
         summary.layers = 1;
-        check_hip(launch_summaries(launch_for(cache, SYNAPSE_KV_KERNEL_PAGE_SELECT, summary.count > 0), summary,
+        check_hip(launch_summaries(launch_for(cache, SYNAPSE_KV_KERNEL_APPEND, summary.count > 0), summary,
                                    dims.precision == SYNAPSE_KV_F16),
                   "key summaries");
     }
@@ -1195,8 +1228,12 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
     check_device_pointer(cache, output, "output");
     // With `append`, qkv stays as the caller wrote it: K is rotated on its way into the pages and Q in registers.
     const bool fused = append && cache.fusable;
+    // Under KV page activation the appended blocks' summaries ride along in the selection launch when no selection
+    // reads them.
+    const bool carry_summaries = append && cache.activation.enabled != 0 && cache.select_jobs > 0 &&
+                                 !cache.select_reads_touched;
     if (append && !fused) {
-        launch_append_layer(cache, layer, const_cast<float*>(qkv), qkv_stride, false);
+        launch_append_layer(cache, layer, const_cast<float*>(qkv), qkv_stride, false, carry_summaries);
     }
     AttentionArgs args{};
     args.geo = geometry(cache, layer);
@@ -1235,8 +1272,18 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
         select.summary_page_bytes = cache.summary_page_bytes;
         select.jobs = reinterpret_cast<const SelectJob*>(cache.blob.pointer + cache.select_offset);
         select.lists = lists;
+        select.keys = cache.select_keys.pointer;
+        select.counters = cache.select_counters.pointer;
+        select.key_stride = static_cast<int32_t>(select_key_stride(cache, cache.most_candidates));
         select.budget = static_cast<int32_t>(cache.activation.budget_pages);
-        check_hip(launch_select(launch_for(cache, SYNAPSE_KV_KERNEL_PAGE_SELECT, true), select, cache.select_jobs, fp16),
+        select.job_count = cache.select_jobs;
+        if (carry_summaries) {
+            select.summary_out = cache.summaries.pointer;
+            select.summary_blocks = reinterpret_cast<const int32_t*>(cache.blob.pointer + cache.touched_offset);
+            select.summary_count = cache.touched_blocks;
+        }
+        check_hip(launch_select(launch_for(cache, SYNAPSE_KV_KERNEL_PAGE_SELECT, true), select, cache.most_candidates,
+                                fp16),
                   "page selection");
     }
     const int prompt_items = cache.prefill_items;
@@ -1538,7 +1585,7 @@ int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPag
                 summary.count = static_cast<int32_t>(blocks.size() / 2);
                 summary.first_layer = 0;
                 summary.layers = static_cast<int32_t>(dims.layers);
-                check_hip(launch_summaries(launch_for(*cache, SYNAPSE_KV_KERNEL_PAGE_SELECT, true), summary,
+                check_hip(launch_summaries(launch_for(*cache, SYNAPSE_KV_KERNEL_APPEND, true), summary,
                                            dims.precision == SYNAPSE_KV_F16),
                           "key summaries");
             }

@@ -194,7 +194,7 @@ inline uint64_t summary_page_elements(int layers, int kv_heads, int page_tokens,
 }
 
 // Recomputes the summaries of `count` (pool page, 64-key block of the page) pairs for layers
-// [first_layer, first_layer + layers) from the stored keys.
+// [first_layer, first_layer + layers) and every KV head from the stored keys.
 struct SummaryArgs {
     Geometry geo;  // geo.layer unused
     uint8_t* summaries;
@@ -229,7 +229,16 @@ struct SelectArgs {
     uint64_t summary_page_bytes;
     const SelectJob* jobs;
     int32_t* lists;
+    uint64_t* keys;      // [jobs][key_stride]: each tile's best min(budget, 64) rank keys, for the job's last tile
+    int32_t* counters;   // [jobs]: tiles of the job done; zero between launches (the last tile resets it)
+    int32_t key_stride;  // tiles of the largest job * min(budget, 64)
     int32_t budget;
+    int32_t job_count;
+    // Summary work riding along (workgroups y >= job_count, x < kv_heads): (page, block) pairs of this layer whose
+    // summaries no job of the launch reads.
+    uint8_t* summary_out;
+    const int32_t* summary_blocks;
+    int32_t summary_count;
     int32_t pad;
 };
 
@@ -261,7 +270,8 @@ int prefill_resident_blocks(int device, int head_dim, int group);
 hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int first, int items, int tiles, bool fp16);
 hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16);
 hipError_t launch_summaries(const Launch& launch, const SummaryArgs& args, bool fp16);
-hipError_t launch_select(const Launch& launch, const SelectArgs& args, int jobs, bool fp16);
+// Key-bound selection (the largest job has `most_candidates` candidates), with args.summary_count summary items.
+hipError_t launch_select(const Launch& launch, const SelectArgs& args, int most_candidates, bool fp16);
 // A projection over `tiles` row tiles (all segments); token tiles of 16 * projection_token_tiles(tokens).
 hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles);
 int projection_token_tiles(int tokens);
