@@ -234,8 +234,8 @@ struct SelectArgs {
     int32_t key_stride;  // tiles of the largest job * min(budget, 64)
     int32_t budget;
     int32_t job_count;
-    // Summary work riding along (workgroups y >= job_count, x < kv_heads): (page, block) pairs of this layer whose
-    // summaries no job of the launch reads.
+    // Summary work riding along (workgroups y < summary_count, x < kv_heads; the jobs follow): (page, block) pairs
+    // of this layer whose summaries no job of the launch reads.
     uint8_t* summary_out;
     const int32_t* summary_blocks;
     int32_t summary_count;
@@ -254,6 +254,9 @@ struct Launch {
 // Dispatches `kernel` for `launch` (hipExtLaunchKernelGGL records the events around the dispatch itself).
 #define SYNAPSE_KV_LAUNCH(kernel, grid, block, launch, ...)                                                       \
     hipExtLaunchKernelGGL(kernel, grid, block, 0, (launch).stream, (launch).start, (launch).stop, 0, __VA_ARGS__)
+// The same with `shared` bytes of dynamic LDS.
+#define SYNAPSE_KV_LAUNCH_SHARED(kernel, grid, block, shared, launch, ...)                                        \
+    hipExtLaunchKernelGGL(kernel, grid, block, shared, (launch).stream, (launch).start, (launch).stop, 0, __VA_ARGS__)
 
 // Launchers (each enqueues at most one kernel and returns the launch status).
 hipError_t launch_table(const Launch& launch, const TableArgs& args);

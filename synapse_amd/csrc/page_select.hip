@@ -24,7 +24,6 @@ namespace {
 
 constexpr int kMaxGroup = 8;
 constexpr int kTileCandidates = 64;
-constexpr int kExtremesStride = 130;  // float2 per channel; rows padded to 16-byte multiples (b128 reads, no conflicts)
 
 __device__ inline void rotate_pair(float x, float y, float c, float s, float& first, float& second) {
 #pragma clang fp contract(off)
@@ -53,27 +52,30 @@ __device__ inline uint64_t rank_key(float bound, int index) {
     return (static_cast<uint64_t>(~ordered) << 12) | static_cast<uint32_t>(index);
 }
 
-struct TileScratch {
-    float2 extremes[kTileCandidates * kExtremesStride];  // [candidate][channel] (min, max), widened
-};
-
+// Elements of one staged candidate row: the block's minimum row, its maximum row, and 16 bytes of padding (rows at
+// a 16-byte stride that spreads the lanes of a wave over the LDS banks).
 template <typename T>
-constexpr size_t select_scratch_bytes() {
-    return sizeof(TileScratch) > sizeof(SummaryScratch<T>) ? sizeof(TileScratch) : sizeof(SummaryScratch<T>);
+__host__ __device__ constexpr int staged_row(int head_dim) {
+    return 2 * head_dim + 16 / static_cast<int>(sizeof(T));
 }
 
-struct MergeScratch {
-    uint64_t keys[kMaxSelectCandidates];     // the tiles' kept keys
-    int32_t chosen[kMaxSelectCandidates];    // block index of each rank below the budget
-};
+// Dynamic LDS of the select kernel: the largest of the tile's staged summaries, a summary work item's scratch, and
+// the last tile's merge (kept keys, then the chosen block of each rank).
+template <typename T>
+size_t select_shared_bytes(int head_dim, int merged, int budget) {
+    const size_t tile = static_cast<size_t>(kTileCandidates) * staged_row<T>(head_dim) * sizeof(T);
+    const size_t merge = static_cast<size_t>(merged) * sizeof(uint64_t) + static_cast<size_t>(budget) * sizeof(int32_t);
+    size_t bytes = sizeof(SummaryScratch<T>);
+    bytes = tile > bytes ? tile : bytes;
+    return merge > bytes ? merge : bytes;
+}
 
-constexpr size_t kSelectScratch = sizeof(TileScratch) > sizeof(MergeScratch) ? sizeof(TileScratch) : sizeof(MergeScratch);
-
-// MathF.Max of the candidate's head bounds, heads in order (KvPageSelector.cs:79-92).
+// MathF.Max of the candidate's head bounds, heads in order (KvPageSelector.cs:79-92). The head bounds are never
+// -0 (see the bound sum), so the hardware maximum agrees with MathF.Max on them.
 __device__ inline float best_bound(const float* head_bounds, int group, int candidate) {
     float best = -__builtin_inff();
     for (int h = 0; h < group; ++h) {
-        best = math_max(best, head_bounds[h * kTileCandidates + candidate]);
+        best = __builtin_fmaxf(best, head_bounds[h * kTileCandidates + candidate]);
     }
     return best;
 }
@@ -85,26 +87,24 @@ __device__ inline float best_bound(const float* head_bounds, int group, int cand
 // them); the job's last tile merges them.
 template <typename T>
 __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
+    extern __shared__ __align__(16) uint8_t scratch[];
     __shared__ __align__(16) float query[kMaxGroup * 128];
-    __shared__ __align__(16) uint8_t scratch[kSelectScratch > select_scratch_bytes<T>() ? kSelectScratch
-                                                                                       : select_scratch_bytes<T>()];
     __shared__ float head_bounds[kMaxGroup * kTileCandidates];
     __shared__ int32_t pages[kTileCandidates];
     __shared__ uint64_t tile_keys[kTileCandidates];
     __shared__ int32_t last_tile;
-    TileScratch& tile = *reinterpret_cast<TileScratch*>(scratch);
-    float2* extremes = tile.extremes;
     const Geometry& g = a.geo;
-    if (static_cast<int>(blockIdx.y) >= a.job_count) {
-        // Summary work: pair blockIdx.y - jobs of this layer, KV head blockIdx.x.
+    if (static_cast<int>(blockIdx.y) < a.summary_count) {
+        // Summary work: pair blockIdx.y of this layer, KV head blockIdx.x.
         if (static_cast<int>(blockIdx.x) < g.kv_heads) {
-            const int pair = blockIdx.y - a.job_count;
+            const int pair = blockIdx.y;
             summarize_block<T>(g, g.layer, blockIdx.x, a.summary_blocks[2 * pair], a.summary_blocks[2 * pair + 1],
                                a.summary_out, a.summary_page_bytes, *reinterpret_cast<SummaryScratch<T>*>(scratch));
         }
         return;
     }
-    const SelectJob job = a.jobs[blockIdx.y];
+    const int job_index = blockIdx.y - a.summary_count;
+    const SelectJob job = a.jobs[job_index];
     const int first = blockIdx.x * kTileCandidates;
     if (first >= job.candidates) {
         return;
@@ -113,7 +113,14 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     const SynapseKvBatchToken token = a.tokens[job.token];
     const int d = g.head_dim;
     const int group = g.group;
-    // 1. The group's query heads, rotated at the token's position when Q in qkv is unrotated.
+    T* staged = reinterpret_cast<T*>(scratch);  // [candidate][staged_row]: minimum row, maximum row
+    const int row_elements = staged_row<T>(d);
+    // 1. The pool pages of the tile's candidates (one table load each).
+    const int32_t* table = g.block_table + static_cast<size_t>(token.slot) * g.pages_per_slot;
+    if (threadIdx.x < count) {
+        pages[threadIdx.x] = table[((first + threadIdx.x + 1) * kBlockKeys) / g.page_tokens];
+    }
+    // 2. The group's query heads, rotated at the token's position when Q in qkv is unrotated.
     const float* row = a.qkv + static_cast<size_t>(job.token) * a.qkv_stride + static_cast<size_t>(job.kv_head) * group * d;
     for (int item = threadIdx.x; item < group * (d / 2); item += blockDim.x) {
         const int h = item / (d / 2);
@@ -128,16 +135,12 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
         query[h * d + i] = x;
         query[h * d + i + d / 2] = y;
     }
-    // 2. The tile's summaries, widened. The pool pages first (one table load per candidate), then the minimum and
-    //    maximum rows of each candidate (2 * head_dim contiguous elements) with 16-byte loads, all issued together.
-    const int32_t* table = g.block_table + static_cast<size_t>(token.slot) * g.pages_per_slot;
-    if (threadIdx.x < count) {
-        pages[threadIdx.x] = table[((first + threadIdx.x + 1) * kBlockKeys) / g.page_tokens];
-    }
     __syncthreads();
+    // 3. The tile's summaries (each candidate's minimum and maximum rows, 2 * head_dim contiguous elements) copied
+    //    to LDS with 16-byte loads, four in flight per thread.
     constexpr int kPerChunk = 16 / static_cast<int>(sizeof(T));
-    const int row_chunks = 2 * d / kPerChunk;  // chunks of one candidate's minimum and maximum rows
-    constexpr int kRounds = 4;  // loads in flight per thread
+    const int row_chunks = 2 * d / kPerChunk;
+    constexpr int kRounds = 4;
     const int items = count * row_chunks;
     for (int batch = 0; batch < items; batch += kRounds * blockDim.x) {
         uint4 loaded[kRounds];
@@ -158,14 +161,7 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
             const int item = batch + threadIdx.x + round * blockDim.x;
             if (item < items) {
                 const int candidate = item / row_chunks;
-                const int element = (item % row_chunks) * kPerChunk;  // the chunk's first element in [min | max]
-                const int which = element / d;
-                const T* values = reinterpret_cast<const T*>(&loaded[round]);
-                float* target = reinterpret_cast<float*>(extremes + candidate * kExtremesStride);
-#pragma unroll
-                for (int e = 0; e < kPerChunk; ++e) {
-                    target[2 * (element % d + e) + which] = widen(values[e]);
-                }
+                reinterpret_cast<uint4*>(staged + candidate * row_elements)[item % row_chunks] = loaded[round];
             }
         }
     }
@@ -174,19 +170,30 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     const int candidate = threadIdx.x % kTileCandidates;
     const int head = threadIdx.x / kTileCandidates;
     if (candidate < count && head < group) {
-        const float4* q = reinterpret_cast<const float4*>(query + head * d);
-        const float4* e = reinterpret_cast<const float4*>(extremes + candidate * kExtremesStride);
+        const float* q = query + head * d;
+        const T* minimum = staged + candidate * row_elements;
+        const T* maximum = minimum + d;
         float sum = 0.0f;
-        // Four channels per round, loaded before the serial sum so the LDS reads of a round overlap.
-        for (int c4 = 0; c4 < d / 4; ++c4) {
+        // The term MathF.Max(q * min, q * max) is q * max for q >= 0 and q * min otherwise: rounding is monotone
+        // and min <= max, so the larger product is that one, bit for bit, except that two zero products may differ
+        // in sign. A zero of either sign added to the running sum leaves it unchanged, since the sum starts at +0
+        // and a round-to-nearest sum is -0 only when both addends are -0. Four channels per round, loaded before
+        // the serial sum so the LDS reads of a round overlap.
+        for (int c0 = 0; c0 < d; c0 += kPerChunk) {
 #pragma clang fp contract(off)
-            const float4 qv = q[c4];
-            const float4 e01 = e[2 * c4];      // (min, max) of channels 4 c4, 4 c4 + 1
-            const float4 e23 = e[2 * c4 + 1];  // (min, max) of channels 4 c4 + 2, 4 c4 + 3
-            sum += math_max(qv.x * e01.x, qv.x * e01.y);
-            sum += math_max(qv.y * e01.z, qv.y * e01.w);
-            sum += math_max(qv.z * e23.x, qv.z * e23.y);
-            sum += math_max(qv.w * e23.z, qv.w * e23.w);
+            T low[kPerChunk];
+            T high[kPerChunk];
+            float qv[kPerChunk];
+            *reinterpret_cast<uint4*>(low) = *reinterpret_cast<const uint4*>(minimum + c0);
+            *reinterpret_cast<uint4*>(high) = *reinterpret_cast<const uint4*>(maximum + c0);
+#pragma unroll
+            for (int j = 0; j < kPerChunk; j += 4) {
+                *reinterpret_cast<float4*>(qv + j) = *reinterpret_cast<const float4*>(q + c0 + j);
+            }
+#pragma unroll
+            for (int j = 0; j < kPerChunk; ++j) {
+                sum += qv[j] * widen(qv[j] >= 0.0f ? high[j] : low[j]);
+            }
         }
         head_bounds[head * kTileCandidates + candidate] = sum;
     }
@@ -197,7 +204,7 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     }
     __syncthreads();
     const int kept_stride = min(a.budget, kTileCandidates);
-    uint64_t* job_keys = a.keys + static_cast<size_t>(blockIdx.y) * a.key_stride;
+    uint64_t* job_keys = a.keys + static_cast<size_t>(job_index) * a.key_stride;
     if (threadIdx.x < count) {
         const uint64_t mine = tile_keys[threadIdx.x];
         int rank = 0;
@@ -213,10 +220,10 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     if (threadIdx.x == 0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const int tiles = (job.candidates + kTileCandidates - 1) / kTileCandidates;
-        const int done = __hip_atomic_fetch_add(a.counters + blockIdx.y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int done = __hip_atomic_fetch_add(a.counters + job_index, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last_tile = done == tiles - 1 ? 1 : 0;
         if (last_tile) {
-            __hip_atomic_store(a.counters + blockIdx.y, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.counters + job_index, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
@@ -224,34 +231,35 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
         return;
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    MergeScratch& merge = *reinterpret_cast<MergeScratch*>(scratch);
     const int tiles = (job.candidates + kTileCandidates - 1) / kTileCandidates;
+    uint64_t* merged_keys = reinterpret_cast<uint64_t*>(scratch);
     int merged = 0;
     for (int t = 0; t < tiles; ++t) {
         const int kept = min(kept_stride, min(kTileCandidates, job.candidates - t * kTileCandidates));
         for (int r = threadIdx.x; r < kept; r += blockDim.x) {
-            merge.keys[merged + r] = job_keys[t * kept_stride + r];
+            merged_keys[merged + r] = job_keys[t * kept_stride + r];
         }
         merged += kept;
     }
+    int32_t* chosen = reinterpret_cast<int32_t*>(merged_keys + merged);  // block index of each rank below budget
     __syncthreads();
     for (int entry = threadIdx.x; entry < merged; entry += blockDim.x) {
-        const uint64_t mine = merge.keys[entry];
+        const uint64_t mine = merged_keys[entry];
         int rank = 0;
         for (int other = 0; other < merged; ++other) {
-            rank += merge.keys[other] < mine ? 1 : 0;
+            rank += merged_keys[other] < mine ? 1 : 0;
         }
         if (rank < a.budget) {
-            merge.chosen[rank] = static_cast<int32_t>(mine & 0xFFF);
+            chosen[rank] = static_cast<int32_t>(mine & 0xFFF);
         }
     }
     __syncthreads();
     // The chosen blocks in ascending order (KvPageSelector marks pages; the list is read in block order).
     for (int r = threadIdx.x; r < a.budget; r += blockDim.x) {
-        const int index = merge.chosen[r];
+        const int index = chosen[r];
         int before = 0;
         for (int other = 0; other < a.budget; ++other) {
-            before += merge.chosen[other] < index ? 1 : 0;
+            before += chosen[other] < index ? 1 : 0;
         }
         a.lists[job.list + 1 + before] = index + 1;
     }
@@ -277,12 +285,29 @@ hipError_t launch_select(const Launch& launch, const SelectArgs& args, int most_
         return hipSuccess;
     }
     const int tiles = (most_candidates + kTileCandidates - 1) / kTileCandidates;
-    const dim3 grid(tiles > args.geo.kv_heads ? tiles : args.geo.kv_heads, args.job_count + args.summary_count);
+    const dim3 grid(tiles > args.geo.kv_heads ? tiles : args.geo.kv_heads, args.summary_count + args.job_count);
     const dim3 block(kTileCandidates * args.geo.group);
+    const int merged = tiles * (args.budget < kTileCandidates ? args.budget : kTileCandidates);
+    // Dynamic LDS may exceed the 64 KiB default (an FP32 tile at head_dim 128 takes 66,560 bytes).
+    static const hipError_t configured = [] {
+        constexpr int kMostDynamic = 96 * 1024;
+        hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel<_Float16>),
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, kMostDynamic);
+        if (status == hipSuccess) {
+            status = hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel<float>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kMostDynamic);
+        }
+        return status;
+    }();
+    if (configured != hipSuccess) {
+        return configured;
+    }
     if (fp16) {
-        SYNAPSE_KV_LAUNCH(select_kernel<_Float16>, grid, block, launch, args);
+        const size_t shared = select_shared_bytes<_Float16>(args.geo.head_dim, merged, args.budget);
+        SYNAPSE_KV_LAUNCH_SHARED(select_kernel<_Float16>, grid, block, shared, launch, args);
     } else {
-        SYNAPSE_KV_LAUNCH(select_kernel<float>, grid, block, launch, args);
+        const size_t shared = select_shared_bytes<float>(args.geo.head_dim, merged, args.budget);
+        SYNAPSE_KV_LAUNCH_SHARED(select_kernel<float>, grid, block, shared, launch, args);
     }
     return hipGetLastError();
 }
