@@ -9,6 +9,7 @@
 
 #include "kv_internal.h"
 #include "page_layout.h"
+#include "page_summary.h"
 
 // hipcc contracts a*b - c*d into a fused multiply-add by default; the rotation must round every product.
 #pragma clang fp contract(off)
@@ -66,8 +67,26 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         if (head >= g.heads) {
             const int kv_head = head - g.heads;
             T* keys = base + (layer_base + kv_head) * region;
-            keys[key_offset<T>(d, within, i)] = to_storage<T>(first);
-            keys[key_offset<T>(d, within, i + half)] = to_storage<T>(second);
+            const T stored_first = to_storage<T>(first);
+            const T stored_second = to_storage<T>(second);
+            keys[key_offset<T>(d, within, i)] = stored_first;
+            keys[key_offset<T>(d, within, i + half)] = stored_second;
+            if (a.extend != nullptr && a.extend[index] != 0) {
+                // The block's summary covers its keys below this position: fold the new key in (MathF.Min /
+                // MathF.Max of KvPageSelector.PageBound), or start from it at the block's first position.
+                T* summary = reinterpret_cast<T*>(a.summaries + static_cast<uint64_t>(page) * a.summary_page_bytes);
+                const int block = within / kBlockKeys;
+                const bool fresh = within % kBlockKeys == 0;
+                const int channels[2] = {i, i + half};
+                const float values[2] = {widen(stored_first), widen(stored_second)};
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    T& minimum = summary[summary_offset(g, g.layer, kv_head, block, 0, channels[c])];
+                    T& maximum = summary[summary_offset(g, g.layer, kv_head, block, 1, channels[c])];
+                    minimum = static_cast<T>(fresh ? values[c] : math_min(widen(minimum), values[c]));
+                    maximum = static_cast<T>(fresh ? values[c] : math_max(widen(maximum), values[c]));
+                }
+            }
         }
     }
 

@@ -274,8 +274,12 @@ struct SynapseKvCache {
     size_t list_layer_entries = 0;   // entries per layer in the blob (random lists differ per layer), else 0
     size_t select_offset = 0;        // key-bound selection jobs
     int32_t select_jobs = 0;
-    size_t touched_offset = 0;       // (page, block) pairs the step writes: their summaries follow each append
+    size_t touched_offset = 0;       // (page, block) pairs whose summaries are recomputed after each append
     int32_t touched_blocks = 0;
+    size_t extend_offset = 0;        // per token: 1 when the append kernel folds the key into its block's summary
+    // Per slot: the length up to which the summary of the slot's last block is exact, where the next append may
+    // fold its key in (-1: not known; the next write recomputes).
+    std::vector<int64_t> fold_next;
     bool select_reads_touched = false;  // a selection ranks a block the step writes (window 0 at a block's end)
     int32_t most_candidates = 0;     // largest key-bound selection job
     synapse_kv::DeviceBuffer<uint64_t> select_keys;
@@ -388,7 +392,10 @@ void shadow_resize(SynapseKvCache& cache, uint32_t slot, uint32_t positions) {
         slot_page(cache, slot, page) = -1;
     }
     cache.capacity[slot] = positions;
-    cache.length[slot] = std::min(cache.length[slot], positions);
+    if (positions < cache.length[slot]) {
+        cache.length[slot] = positions;
+        cache.fold_next[slot] = -1;
+    }
 }
 
 void check_slot(const SynapseKvCache& cache, uint32_t slot) {
@@ -516,7 +523,8 @@ size_t select_key_stride(const SynapseKvCache& cache, int32_t most_candidates) {
 // split into work items of at most `chunk` keys whose partial rows the merge kernel combines. The chunk is the
 // prefill_split_keys option when set, otherwise chosen by choose_prefill_chunk: runs that already fill the device
 // are not split (and need no merge), short chunks over long caches are.
-void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t count) {
+void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t count,
+               const std::vector<uint32_t>& old_lengths) {
     const Dims& dims = cache.dims;
     const int32_t group = static_cast<int32_t>(dims.heads / dims.kv_heads);
     // A row: keys [key_begin, keys) of one (token, KV head), or of a shared set's members (set >= 0, token -1).
@@ -715,28 +723,70 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         }
     }
 
-    // Blocks the step writes (after copy-on-write), whose summaries each layer recomputes after its appends. A
-    // decode unit's candidates end below its window, so the step's own blocks are candidates only with no window
-    // at a block's last position; otherwise the summary work can ride along in the selection launch.
+    // Summary upkeep of the blocks the step writes (after copy-on-write). A token alone in its block that appends
+    // at its slot's exact length (fold_next) is folded into the summary by the append kernel; every other written
+    // block is recomputed after the appends from its keys below the slot's new length, which leaves it exact for
+    // the next append when the slot's positions this step were exactly [old length, new length). A decode unit's
+    // candidates end below its window, so a block the step writes is a candidate only with no window at a block's
+    // last position; otherwise a recomputation can ride along in the selection launch.
     std::vector<int32_t> touched;
+    std::vector<int32_t> extend;
     bool select_reads_touched = false;
     if (activation.enabled != 0) {
-        std::vector<int64_t> keys;  // page * 65536 + block
-        for (int32_t index = 0; index < count; ++index) {
+        auto block_key = [&](int32_t index) {
             const uint32_t position = static_cast<uint32_t>(tokens[index].position);
             const int32_t page = cache.table[static_cast<size_t>(tokens[index].slot) * dims.pages_per_slot +
                                              position / dims.page_tokens];
-            keys.push_back(static_cast<int64_t>(page) * 65536 + (position % dims.page_tokens) / kStepKeys);
-            const Unit& unit = units[index];
-            if (unit.window_page >= 0 && unit.window_page - 1 >= static_cast<int32_t>(position / kStepKeys)) {
-                select_reads_touched = true;
+            return static_cast<int64_t>(page) * 65536 + (position % dims.page_tokens) / kStepKeys;
+        };
+        std::vector<int64_t> keys(count);
+        for (int32_t index = 0; index < count; ++index) {
+            keys[index] = block_key(index);
+        }
+        std::vector<int64_t> sorted = keys;
+        std::sort(sorted.begin(), sorted.end());
+        std::vector<int32_t> in_slot(dims.slots, 0);
+        for (int32_t index = 0; index < count; ++index) {
+            ++in_slot[tokens[index].slot];
+        }
+        extend.assign(count, 0);
+        std::vector<std::pair<int64_t, int32_t>> recompute;  // (block key, keys below the slot's new length)
+        std::vector<int64_t> lowest(dims.slots, INT64_MAX);
+        std::vector<int32_t> written(dims.slots, 0);
+        for (int32_t index = 0; index < count; ++index) {
+            lowest[tokens[index].slot] = std::min<int64_t>(lowest[tokens[index].slot], tokens[index].position);
+            ++written[tokens[index].slot];
+        }
+        for (int32_t index = 0; index < count; ++index) {
+            const int32_t slot = tokens[index].slot;
+            const int64_t position = tokens[index].position;
+            const auto range = std::equal_range(sorted.begin(), sorted.end(), keys[index]);
+            const bool solo = range.second - range.first == 1 && in_slot[slot] == 1;
+            if (solo && (position % kStepKeys == 0 || position == cache.fold_next[slot])) {
+                extend[index] = 1;
+            } else {
+                const int64_t start = position / kStepKeys * kStepKeys;
+                recompute.emplace_back(keys[index],
+                                       static_cast<int32_t>(std::min<int64_t>(kStepKeys, cache.length[slot] - start)));
+                const Unit& unit = units[index];
+                if (unit.window_page >= 0 && unit.window_page - 1 >= static_cast<int32_t>(position / kStepKeys)) {
+                    select_reads_touched = true;
+                }
             }
         }
-        std::sort(keys.begin(), keys.end());
-        keys.erase(std::unique(keys.begin(), keys.end()), keys.end());
-        for (int64_t key : keys) {
+        // A slot whose positions this step are exactly [old length, new length) stays exact at its new length.
+        for (int32_t index = 0; index < count; ++index) {
+            const int32_t slot = tokens[index].slot;
+            const bool contiguous = lowest[slot] == old_lengths[slot] &&
+                                    cache.length[slot] - old_lengths[slot] == static_cast<uint32_t>(written[slot]);
+            cache.fold_next[slot] = contiguous ? static_cast<int64_t>(cache.length[slot]) : -1;
+        }
+        std::sort(recompute.begin(), recompute.end());
+        recompute.erase(std::unique(recompute.begin(), recompute.end()), recompute.end());
+        for (const auto& [key, valid] : recompute) {
             touched.push_back(static_cast<int32_t>(key / 65536));
             touched.push_back(static_cast<int32_t>(key % 65536));
+            touched.push_back(valid);
         }
     }
 
@@ -942,7 +992,8 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.lists_offset = align_up(cache.prefill_offset + prefill.size() * sizeof(PrefillItem), 256);
     cache.select_offset = align_up(cache.lists_offset + lists.size() * sizeof(int32_t), 256);
     cache.touched_offset = align_up(cache.select_offset + select_jobs.size() * sizeof(SelectJob), 256);
-    const size_t total = cache.touched_offset + touched.size() * sizeof(int32_t);
+    cache.extend_offset = align_up(cache.touched_offset + touched.size() * sizeof(int32_t), 256);
+    const size_t total = cache.extend_offset + extend.size() * sizeof(int32_t);
     cache.select_keys.ensure(select_jobs.size() * select_key_stride(cache, most_candidates), "page selection keys");
     if (select_jobs.size() > cache.select_counters.count) {
         cache.select_counters.ensure(std::max<size_t>(select_jobs.size(), 256), "page selection counters");
@@ -963,6 +1014,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     std::memcpy(staging + cache.lists_offset, lists.data(), lists.size() * sizeof(int32_t));
     std::memcpy(staging + cache.select_offset, select_jobs.data(), select_jobs.size() * sizeof(SelectJob));
     std::memcpy(staging + cache.touched_offset, touched.data(), touched.size() * sizeof(int32_t));
+    std::memcpy(staging + cache.extend_offset, extend.data(), extend.size() * sizeof(int32_t));
     cache.uploader.copy(cache.blob.pointer, total, cache.stream);
     cache.step_count = count;
     cache.decode_workers = workers;
@@ -974,7 +1026,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     cache.list_layer_entries = random ? static_cast<size_t>(list_entries) : 0;
     cache.select_jobs = static_cast<int32_t>(select_jobs.size());
     cache.most_candidates = most_candidates;
-    cache.touched_blocks = static_cast<int32_t>(touched.size() / 2);
+    cache.touched_blocks = static_cast<int32_t>(touched.size() / 3);
     cache.select_reads_touched = select_reads_touched;
     // The fused append + decode launch needs every token to own its slot (no token may read another token's
     // position of the same step, and each (token, KV head) row appends its own position only) and no prompt run
@@ -1053,6 +1105,7 @@ void create_cache(const SynapseKvDesc& desc, SynapseKvCache** output) {
         set_device(*cache);
         cache->capacity.assign(dims.slots, 0);
         cache->length.assign(dims.slots, 0);
+        cache->fold_next.assign(dims.slots, -1);
         cache->table.assign(static_cast<size_t>(dims.slots) * dims.pages_per_slot, -1);
         cache->refcount.assign(dims.max_pages, 0);
         cache->free_stack.resize(dims.max_pages);
@@ -1189,6 +1242,11 @@ void launch_append_layer(SynapseKvCache& cache, uint32_t layer, float* qkv, uint
     args.cosines = cache.cosines.pointer;
     args.sines = cache.sines.pointer;
     args.write_back = write_back ? 1 : 0;
+    if (cache.activation.enabled != 0) {
+        args.summaries = cache.summaries.pointer;
+        args.summary_page_bytes = cache.summary_page_bytes;
+        args.extend = reinterpret_cast<const int32_t*>(cache.blob.pointer + cache.extend_offset);
+    }
     check_hip(launch_append(launch_for(cache, SYNAPSE_KV_KERNEL_APPEND, cache.step_count > 0), args, cache.step_count,
                             dims.precision == SYNAPSE_KV_F16),
               "append");
@@ -1456,6 +1514,7 @@ int32_t synapse_kv_release(SynapseKvCache* cache, uint32_t slot) {
         set_device(*cache);
         shadow_resize(*cache, slot, 0);
         cache->length[slot] = 0;
+        cache->fold_next[slot] = -1;
         flush_ops(*cache);
     });
 }
@@ -1471,6 +1530,7 @@ int32_t synapse_kv_truncate(SynapseKvCache* cache, uint32_t slot, uint32_t lengt
                     std::to_string(cache->length[slot]));
         }
         cache->length[slot] = length;
+        cache->fold_next[slot] = -1;  // the block summary covers keys past the new length: recompute on the next write
     });
 }
 
@@ -1493,6 +1553,7 @@ int32_t synapse_kv_fork(SynapseKvCache* cache, uint32_t source, uint32_t target)
         }
         cache->capacity[target] = std::min(dims.max_positions, shared * dims.page_tokens);
         cache->length[target] = cache->length[source];
+        cache->fold_next[target] = -1;
         if (shared != 0) {
             set_device(*cache);
             cache->ops.push_back(TableOp{kOpFork, static_cast<int32_t>(source), static_cast<int32_t>(target),
@@ -1516,10 +1577,11 @@ int32_t synapse_kv_step_prompt(SynapseKvCache* cache, const SynapseKvBatchToken*
         }
         set_device(*cache);
         cache->step_ready = false;
+        const std::vector<uint32_t> old_lengths = cache->length;
         prepare_step(*cache, tokens, static_cast<int32_t>(count));
         flush_ops(*cache);
         cache->prompt_start = static_cast<int32_t>(prompt_start);
-        plan_step(*cache, tokens, static_cast<int32_t>(count));
+        plan_step(*cache, tokens, static_cast<int32_t>(count), old_lengths);
     });
 }
 
@@ -1560,7 +1622,8 @@ int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPag
             cache->summaries.ensure(cache->summary_page_bytes * dims.max_pages, "key summaries");
         }
         if (rebuild) {
-            // Summaries of every block of every mapped page, all layers.
+            // Summaries of every block of every mapped page, all layers; fold chains start again at block starts.
+            std::fill(cache->fold_next.begin(), cache->fold_next.end(), -1);
             const Dims& dims = cache->dims;
             std::vector<int32_t> blocks;
             for (uint32_t page = 0; page < dims.max_pages; ++page) {
@@ -1568,6 +1631,7 @@ int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPag
                     for (uint32_t block = 0; block < dims.page_tokens / kStepKeys; ++block) {
                         blocks.push_back(static_cast<int32_t>(page));
                         blocks.push_back(static_cast<int32_t>(block));
+                        blocks.push_back(kStepKeys);
                     }
                 }
             }
@@ -1582,7 +1646,7 @@ int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPag
                 summary.summaries = cache->summaries.pointer;
                 summary.summary_page_bytes = cache->summary_page_bytes;
                 summary.blocks = reinterpret_cast<const int32_t*>(cache->op_blob.pointer);
-                summary.count = static_cast<int32_t>(blocks.size() / 2);
+                summary.count = static_cast<int32_t>(blocks.size() / 3);
                 summary.first_layer = 0;
                 summary.layers = static_cast<int32_t>(dims.layers);
                 check_hip(launch_summaries(launch_for(*cache, SYNAPSE_KV_KERNEL_APPEND, true), summary,

@@ -121,6 +121,13 @@ struct AppendArgs {
     const float* cosines;
     const float* sines;
     int32_t write_back;  // 1: rotated Q and K replace the qkv values; 0: qkv is left as it was
+    // KV page activation: a token with extend[token] != 0 is alone in its 64-key block in the step and appends
+    // right after its slot's keys, whose block summary covers exactly the keys below it, so the append kernel folds
+    // the new key in (or starts the summary at a block's first position). Other written blocks are recomputed from
+    // their keys below the slot's new length. Null: no summaries.
+    uint8_t* summaries;
+    uint64_t summary_page_bytes;
+    const int32_t* extend;
 };
 
 struct AttentionArgs {
@@ -193,13 +200,13 @@ inline uint64_t summary_page_elements(int layers, int kv_heads, int page_tokens,
     return static_cast<uint64_t>(layers) * kv_heads * (page_tokens / 64) * 2 * head_dim;
 }
 
-// Recomputes the summaries of `count` (pool page, 64-key block of the page) pairs for layers
-// [first_layer, first_layer + layers) and every KV head from the stored keys.
+// Recomputes the summaries of `count` (pool page, 64-key block of the page, keys 1..64) items for layers
+// [first_layer, first_layer + layers) and every KV head from the block's first `keys` stored keys.
 struct SummaryArgs {
     Geometry geo;  // geo.layer unused
     uint8_t* summaries;
     uint64_t summary_page_bytes;
-    const int32_t* blocks;  // (page, block) pairs
+    const int32_t* blocks;  // (page, block, keys) triples
     int32_t count;
     int32_t first_layer;
     int32_t layers;
@@ -234,8 +241,8 @@ struct SelectArgs {
     int32_t key_stride;  // tiles of the largest job * min(budget, 64)
     int32_t budget;
     int32_t job_count;
-    // Summary work riding along (workgroups y < summary_count, x < kv_heads; the jobs follow): (page, block) pairs
-    // of this layer whose summaries no job of the launch reads.
+    // Summary work riding along (workgroups y < summary_count, x < kv_heads; the jobs follow): (page, block, keys)
+    // triples of this layer whose summaries no job of the launch reads.
     uint8_t* summary_out;
     const int32_t* summary_blocks;
     int32_t summary_count;

@@ -31,14 +31,14 @@ __device__ inline void rotate_pair(float x, float y, float c, float s, float& fi
     second = x * s + y * c;
 }
 
-// Grid (pairs, layers, kv_heads) of 256 threads: the summary of one (page, block) pair, layer and KV head.
+// Grid (items, layers, kv_heads) of 256 threads: the summary of one (page, block, keys) item's first keys, layer and
+// KV head.
 template <typename T>
 __global__ __launch_bounds__(256) void summary_kernel(SummaryArgs a) {
     __shared__ SummaryScratch<T> scratch;
-    const int page = a.blocks[2 * blockIdx.x];
-    const int block = a.blocks[2 * blockIdx.x + 1];
-    summarize_block<T>(a.geo, a.first_layer + blockIdx.y, blockIdx.z, page, block, a.summaries, a.summary_page_bytes,
-                       scratch);
+    const int32_t* item = a.blocks + 3 * blockIdx.x;
+    summarize_block<T>(a.geo, a.first_layer + blockIdx.y, blockIdx.z, item[0], item[1], item[2], a.summaries,
+                       a.summary_page_bytes, scratch);
 }
 
 // Sort key of a candidate, 44 bits: ascending order = bound descending (float.CompareTo: NaN below every number, -0
@@ -97,9 +97,9 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     if (static_cast<int>(blockIdx.y) < a.summary_count) {
         // Summary work: pair blockIdx.y of this layer, KV head blockIdx.x.
         if (static_cast<int>(blockIdx.x) < g.kv_heads) {
-            const int pair = blockIdx.y;
-            summarize_block<T>(g, g.layer, blockIdx.x, a.summary_blocks[2 * pair], a.summary_blocks[2 * pair + 1],
-                               a.summary_out, a.summary_page_bytes, *reinterpret_cast<SummaryScratch<T>*>(scratch));
+            const int32_t* item = a.summary_blocks + 3 * blockIdx.y;
+            summarize_block<T>(g, g.layer, blockIdx.x, item[0], item[1], item[2], a.summary_out, a.summary_page_bytes,
+                               *reinterpret_cast<SummaryScratch<T>*>(scratch));
         }
         return;
     }

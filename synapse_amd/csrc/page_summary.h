@@ -1,5 +1,5 @@
 // Key summaries of KV page activation (ADR-016): per (pool page, layer, KV head, 64-key block) the per-channel
-// minimum and maximum of the stored keys, kept in the storage type (exact). KvPageSelector.PageBound
+// minimum and maximum of the block's keys below the writing slot's length, kept in the storage type (exact). KvPageSelector.PageBound
 // (src/Synapse.Runtime/Features/TextGeneration/KvPageSelector.cs:57-78) reduces the page's keys with MathF.Min and
 // MathF.Max; both are exact and, for the non-NaN values keys hold, independent of the order of the keys.
 #pragma once
@@ -55,12 +55,13 @@ struct SummaryScratch {
     float partial[2][512];
 };
 
-// Summary of block `block` of pool page `page` (layer, kv_head) from the stored keys, by the whole workgroup
-// (blockDim.x a multiple of 64, at most 512): the block's keys are copied to LDS with 16-byte loads, the keys of
-// each channel are reduced in shares of 64 / shares keys, and the shares combined. Starts and ends with a barrier.
+// Summary of the first `valid` (1..64) keys of block `block` of pool page `page` (layer, kv_head), by the whole
+// workgroup (blockDim.x a multiple of 64, at most 512): the block's keys are copied to LDS with 16-byte loads, the
+// keys of each channel are reduced in shares of 64 / shares keys, and the shares combined. Starts and ends with a
+// barrier.
 template <typename T>
-__device__ void summarize_block(const Geometry& g, int layer, int kv_head, int page, int block, uint8_t* summaries,
-                                uint64_t summary_page_bytes, SummaryScratch<T>& scratch) {
+__device__ void summarize_block(const Geometry& g, int layer, int kv_head, int page, int block, int valid,
+                                uint8_t* summaries, uint64_t summary_page_bytes, SummaryScratch<T>& scratch) {
     const int d = g.head_dim;
     const T* region = reinterpret_cast<const T*>(g.pool + static_cast<uint64_t>(page) * g.page_bytes) +
                       ((static_cast<size_t>(layer) * 2) * g.kv_heads + kv_head) * static_cast<size_t>(g.page_tokens) * d;
@@ -78,9 +79,11 @@ __device__ void summarize_block(const Geometry& g, int layer, int kv_head, int p
     for (int item = threadIdx.x; item < d * shares; item += blockDim.x) {
         const int channel = item % d;
         const int share = item / d;
-        float minimum = widen(scratch.keys[key_offset<T>(d, share * per_share, channel)]);
-        float maximum = minimum;
-        for (int key = share * per_share + 1; key < (share + 1) * per_share; ++key) {
+        // Unwritten keys are left out; a share holding none keeps (+inf, -inf), which the combination ignores.
+        float minimum = __builtin_inff();
+        float maximum = -__builtin_inff();
+        const int stop = min((share + 1) * per_share, valid);
+        for (int key = share * per_share; key < stop; ++key) {
             const float value = widen(scratch.keys[key_offset<T>(d, key, channel)]);
             minimum = math_min(minimum, value);
             maximum = math_max(maximum, value);

@@ -218,3 +218,46 @@ def test_page_activation_arguments(torch_gpu):
     with pytest.raises(InvalidOperationError, match="prompt_start"):
         cache.step([(0, 0)], prompt_start=2)
     cache.close()
+
+
+def test_long_lists_take_the_even_split(torch_gpu):
+    """A budget of 270 pages over an 18,000-position slot gives rows of 273 listed blocks, cut over many decode
+    waves and merged (partial rows of one row in several merge levels), next to a slot with a short list."""
+    say("page activation long lists")
+    pair = PagePair(torch_gpu, page=256, growth=1024, max_positions=20480, slots=2, max_pages=2 * 80 + 8,
+                    step_tokens=1024)
+    rng = np.random.default_rng(6)
+    for slot, length in ((0, 18000), (1, 3000)):
+        for first in range(0, length, 1024):
+            tokens = [(slot, p) for p in range(first, min(length, first + 1024))]
+            assert pair.cpu.step(tokens) == 0
+            pair.gpu.step(tokens)
+            for layer in range(pair.layers):
+                rows = rng.standard_normal((len(tokens), pair.width)).astype(np.float32)
+                pair.gpu.append_rope(layer, torch_gpu.from_numpy(rows.copy()).cuda())
+                assert pair.cpu.append_rope(layer, rows, pair.cos, pair.sin) == 0
+    pair.activate(270, 64)
+    pair.run([(0, 18000), (1, 3000)], rng, expect_sparse=True)
+    pair.run([(0, 18001), (1, 3001)], rng, fused=True, expect_sparse=True)
+
+
+def test_folded_summaries_through_block_ends_and_truncation(torch_gpu):
+    """One token per step from position 300: the first step after activation recomputes its block from the keys
+    below the new length, later steps fold each key into the summary; with no window every completed block is a
+    candidate at once (positions 383 and 447 rank the block they complete). After a truncation the next append
+    recomputes (the summary covered keys past the new length), then folding resumes; a two-token step and a step
+    that overwrites an earlier position recompute too."""
+    say("page activation folds")
+    pair = PagePair(torch_gpu, page=128, max_positions=1024, slots=2, max_pages=24)
+    rng = np.random.default_rng(8)
+    prefill(pair, rng, [(0, 300)])
+    pair.activate(2, 0)
+    for position in range(300, 460):
+        pair.run([(0, position)], rng, expect_sparse=True)
+    pair.call("truncate", 0, 430)
+    for position in range(430, 470):
+        pair.run([(0, position)], rng, expect_sparse=True)
+    pair.run([(0, 470), (0, 471)], rng, prompt_start=0)
+    for position in range(472, 480):
+        pair.run([(0, position)], rng, expect_sparse=True)
+    pair.check_contents(0)
