@@ -303,6 +303,101 @@ int32_t synapse_kv_project(SynapseKvWeights* weights, const SynapseKvProjection*
  * at least that many bytes (read-back for checks). */
 int32_t synapse_kv_weights_read(SynapseKvWeights* weights, uint32_t index, uint8_t* blocks, uint64_t bytes);
 
+/* ---- The dense decoder step (libsynapse_gpu's model API, ffi.rs:106-271; decoder.rs:60-136) ----
+ * A pre-norm decoder over caller-owned mapped weights: per layer RMS norm, Q/K/V projections with optional
+ * biases, NeoX RoPE + KV append, grouped-query attention, the output projection added to the residual, RMS norm,
+ * gate and up projections, SwiGLU, the down projection added to the residual; then the output norm and the logits
+ * projection for the step's logits rows (step.rs:137-185, step/layers.rs). Built from the handles above: one KV
+ * cache and one weights handle, on one stream. */
+
+#define SYNAPSE_KV_NO_TENSOR 0xFFFFFFFFFFFFFFFFull /* NO_TENSOR: an optional tensor the model does not have */
+#define SYNAPSE_KV_ENCODING_Q8_0 8u               /* GGML type IDs (ADR-021); Q4_K (12) and Q6_K (14) are UNAVAILABLE */
+#define SYNAPSE_KV_ALL_Q8_0 0x08888888ull         /* DecoderLayerOffsets.encodings with every matrix in Q8_0 */
+#define SYNAPSE_KV_ROPE_NEOX 0u
+#define SYNAPSE_KV_ACTIVATION_SWIGLU 0u
+
+/* DecoderLayerOffsets (decoder.rs:60-81): byte offsets of one block's tensors in the mapped weights. Norm weights
+ * and biases are FP32; matrices are GGML blocks in the encoding packed four bits per matrix (Q, K, V, O, gate, up,
+ * down from the lowest) in `encodings`. */
+typedef struct SynapseKvLayerOffsets {
+    uint64_t attention_norm;
+    uint64_t query;
+    uint64_t key;
+    uint64_t value;
+    uint64_t query_bias;        /* or SYNAPSE_KV_NO_TENSOR */
+    uint64_t key_bias;          /* or SYNAPSE_KV_NO_TENSOR */
+    uint64_t value_bias;        /* or SYNAPSE_KV_NO_TENSOR */
+    uint64_t query_norm;        /* SYNAPSE_KV_NO_TENSOR (per-head Q/K norms are UNAVAILABLE, as in the reference) */
+    uint64_t key_norm;          /* SYNAPSE_KV_NO_TENSOR */
+    uint64_t attention_output;
+    uint64_t feed_forward_norm;
+    uint64_t gate;
+    uint64_t up;
+    uint64_t down;
+    uint64_t encodings;
+} SynapseKvLayerOffsets;
+
+/* DecoderDesc (decoder.rs:85-116): pointers stay owned by the caller while the model lives. */
+typedef struct SynapseKvDecoderDesc {
+    const uint8_t* weights;
+    uint64_t weights_length;
+    const SynapseKvLayerOffsets* layers;
+    const float* rope_cosines;  /* [context][head_dim / 2] */
+    const float* rope_sines;
+    uint64_t token_embedding;   /* vocabulary x hidden matrix */
+    uint64_t output_norm;       /* FP32 [hidden] */
+    uint64_t output;            /* vocabulary x hidden matrix */
+    uint32_t layer_count;
+    uint32_t hidden;            /* heads * head_dim */
+    uint32_t feed_forward;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;          /* 64 or 128 */
+    uint32_t vocabulary;
+    uint32_t context;
+    uint32_t session_slots;
+    uint32_t step_tokens;
+    uint32_t logits_rows;
+    float rms_epsilon;
+    uint32_t embedding_encoding;
+    uint32_t rope_layout;       /* SYNAPSE_KV_ROPE_NEOX */
+    uint32_t activation;        /* SYNAPSE_KV_ACTIVATION_SWIGLU */
+    uint32_t kv_precision;      /* SYNAPSE_KV_F32 or SYNAPSE_KV_F16 */
+    uint32_t kv_growth_positions;
+    uint32_t output_encoding;
+} SynapseKvDecoderDesc;
+
+typedef struct SynapseKvDecoder SynapseKvDecoder;
+
+/* synapse_gpu_decoder_create (ffi.rs:106-137) with DecoderPlan::new's validation (decoder/checks.rs): status 2
+ * for inconsistent shapes and out-of-range or misaligned tensors, 3 for what the kernels do not implement
+ * (encodings other than Q8_0, RoPE layouts other than NeoX, activations other than SwiGLU, per-head Q/K norms,
+ * head dimensions other than 64 and 128, more than 8 query heads per KV head). Uploads the matrices (repacked), the
+ * norms, biases and the embedding table to device memory on `device`; the KV page pool takes the pages every slot
+ * needs at full context, or what fits in free device memory. */
+int32_t synapse_kv_decoder_create(const SynapseKvDecoderDesc* desc, int32_t device, SynapseKvDecoder** model);
+
+/* synapse_gpu_decoder_forward (ffi.rs:172-211): one batched step of `count` tokens; the tokens' logits rows must
+ * be 0..k-1 in token order (BatchDecoding.cs:24-27) with k <= logits_rows, and `logits` (host memory) receives
+ * k * vocabulary floats. Returns after the logits are copied. */
+int32_t synapse_kv_decoder_forward(SynapseKvDecoder* model, const SynapseKvBatchToken* tokens, size_t count,
+                                   float* logits, size_t logits_capacity);
+
+/* synapse_kv_decoder_forward with the step's prompt boundary (IBatchDecoder.Forward(tokens, promptStart)), which
+ * KV page activation uses; synapse_kv_decoder_forward passes prompt_start = count. */
+int32_t synapse_kv_decoder_forward_prompt(SynapseKvDecoder* model, const SynapseKvBatchToken* tokens, size_t count,
+                                          size_t prompt_start, float* logits, size_t logits_capacity);
+
+/* synapse_gpu_decoder_destroy / _kv_bytes / _reserve (ffi.rs:213-271). */
+void synapse_kv_decoder_destroy(SynapseKvDecoder* model);
+uint64_t synapse_kv_decoder_kv_bytes(const SynapseKvDecoder* model);
+int32_t synapse_kv_decoder_reserve(SynapseKvDecoder* model, uint32_t slot, uint32_t positions);
+
+/* The model's KV cache and stream: options, KV page activation, fork/truncate/release and the read-backs work on
+ * the returned cache (owned by the model). */
+int32_t synapse_kv_decoder_cache(SynapseKvDecoder* model, SynapseKvCache** cache);
+int32_t synapse_kv_decoder_set_stream(SynapseKvDecoder* model, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 
@@ -314,6 +409,8 @@ static_assert(sizeof(SynapseKvProfile) == 128, "SynapseKvProfile is pinned at 12
 static_assert(sizeof(SynapseKvMatrix) == 24, "SynapseKvMatrix is pinned at 24 bytes");
 static_assert(sizeof(SynapseKvPageActivation) == 24, "SynapseKvPageActivation is pinned at 24 bytes");
 static_assert(sizeof(SynapseKvProjection) == 48, "SynapseKvProjection is pinned at 48 bytes");
+static_assert(sizeof(SynapseKvLayerOffsets) == 120, "SynapseKvLayerOffsets is pinned at 120 bytes");
+static_assert(sizeof(SynapseKvDecoderDesc) == 136, "SynapseKvDecoderDesc is pinned at 136 bytes");
 #else
 _Static_assert(sizeof(SynapseKvDeviceInfo) == 152, "SynapseKvDeviceInfo is pinned at 152 bytes");
 _Static_assert(sizeof(SynapseKvBatchToken) == 16, "SynapseKvBatchToken is pinned at 16 bytes");
@@ -323,6 +420,8 @@ _Static_assert(sizeof(SynapseKvProfile) == 128, "SynapseKvProfile is pinned at 1
 _Static_assert(sizeof(SynapseKvMatrix) == 24, "SynapseKvMatrix is pinned at 24 bytes");
 _Static_assert(sizeof(SynapseKvPageActivation) == 24, "SynapseKvPageActivation is pinned at 24 bytes");
 _Static_assert(sizeof(SynapseKvProjection) == 48, "SynapseKvProjection is pinned at 48 bytes");
+_Static_assert(sizeof(SynapseKvLayerOffsets) == 120, "SynapseKvLayerOffsets is pinned at 120 bytes");
+_Static_assert(sizeof(SynapseKvDecoderDesc) == 136, "SynapseKvDecoderDesc is pinned at 136 bytes");
 #endif
 
 #endif /* SYNAPSE_KV_H */

@@ -1565,3 +1565,182 @@ void orc_prefix_remember(void* handle, const int32_t* prompt, int count, const i
 void orc_prefix_clear(void* handle) { static_cast<Prefix*>(handle)->tokens.clear(); }
 
 }  // extern "C"
+
+// ---- The dense decoder step ---------------------------------------------------------------------------------
+
+// encode_step (native/synapse-gpu/src/Features/GpuKernels/step.rs:137-185) over the kernels' semantics: embedding
+// lookup, RMS norm and SwiGLU as elementwise.cu:3-109, Q8_0 projections in matmul.cu's FP32 order
+// (q8_matvec_row), NeoX RoPE + KV append and attention through the paged restatement above (orc_paged_*), the
+// output and down projections added to the residual (step/layers.rs:62-206), and the logits rows normalized by
+// the output norm and projected (step/layers.rs:208-228).
+namespace {
+
+struct DecoderOracle {
+    const uint8_t* weights;
+    std::vector<uint64_t> layers;  // layer_count x 15 offsets (DecoderLayerOffsets order)
+    uint64_t token_embedding, output_norm, output;
+    int layer_count, hidden, feed_forward, heads, kv_heads, head_dim, vocabulary;
+    float epsilon;
+    std::vector<float> cosines, sines;
+    void* cache;
+};
+
+constexpr uint64_t kNoTensor = ~0ull;
+
+const float* f32_at(const DecoderOracle& m, uint64_t offset) {
+    return reinterpret_cast<const float*>(m.weights + offset);
+}
+
+// synapse_rms_norm (elementwise.cu:17-52): the sum of squares, then x * (1 / sqrt(mean + eps)) * w.
+void rms_norm_row(const float* x, const float* w, int columns, float epsilon, float* y) {
+    float sum = 0.0f;
+    for (int i = 0; i < columns; ++i) {
+        sum += x[i] * x[i];
+    }
+    const float scale = 1.0f / std::sqrt(sum / static_cast<float>(columns) + epsilon);
+    for (int i = 0; i < columns; ++i) {
+        y[i] = x[i] * scale * w[i];
+    }
+}
+
+// Rows of one Q8_0 matrix (rows x columns at `offset`) times input rows, plus an optional FP32 bias, into
+// output[t * out_stride + out_column + row] (added to it when accumulating).
+void project_rows(const DecoderOracle& m, uint64_t offset, uint64_t bias, int rows, int columns, int tokens,
+                  const float* input, int in_stride, float* output, int out_stride, int out_column, bool accumulate,
+                  int threads) {
+    const int blocks = columns / 32;
+    const size_t row_bytes = static_cast<size_t>(blocks) * 34;
+    const float* biases = bias == kNoTensor ? nullptr : f32_at(m, bias);
+    Pool::run(rows, threads, [&](int, int row) {
+        const uint8_t* weights = m.weights + offset + row * row_bytes;
+        for (int t = 0; t < tokens; ++t) {
+            float total = q8_matvec_row(weights, blocks, input + static_cast<size_t>(t) * in_stride);
+            if (biases != nullptr) {
+                total += biases[row];
+            }
+            float& destination = output[static_cast<size_t>(t) * out_stride + out_column + row];
+            destination = accumulate ? destination + total : total;
+        }
+    });
+}
+
+}  // namespace
+
+extern "C" {
+
+// dims: layer_count, hidden, feed_forward, heads, kv_heads, head_dim, vocabulary, context, session_slots,
+// step_tokens, kv_precision, kv_growth_positions, page_tokens, max_pages. top: token_embedding, output_norm,
+// output. layers: layer_count x 15 offsets. The weights stay owned by the caller.
+void* orc_decoder_create(const uint8_t* weights, const uint64_t* layers, const uint64_t* top, const int* dims,
+                         float epsilon, const float* cosines, const float* sines) {
+    auto* m = new DecoderOracle{};
+    m->weights = weights;
+    m->layer_count = dims[0];
+    m->hidden = dims[1];
+    m->feed_forward = dims[2];
+    m->heads = dims[3];
+    m->kv_heads = dims[4];
+    m->head_dim = dims[5];
+    m->vocabulary = dims[6];
+    const int context = dims[7];
+    m->layers.assign(layers, layers + static_cast<size_t>(m->layer_count) * 15);
+    m->token_embedding = top[0];
+    m->output_norm = top[1];
+    m->output = top[2];
+    m->epsilon = epsilon;
+    m->cosines.assign(cosines, cosines + static_cast<size_t>(context) * (m->head_dim / 2));
+    m->sines.assign(sines, sines + static_cast<size_t>(context) * (m->head_dim / 2));
+    m->cache = orc_paged_create(m->layer_count, m->heads, m->kv_heads, m->head_dim, context, dims[11], dims[12], dims[10],
+                                dims[8], dims[13], dims[9]);
+    if (m->cache == nullptr) {
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+void orc_decoder_destroy(void* handle) {
+    auto* m = static_cast<DecoderOracle*>(handle);
+    orc_paged_destroy(m->cache);
+    delete m;
+}
+
+void* orc_decoder_cache(void* handle) { return static_cast<DecoderOracle*>(handle)->cache; }
+
+// One step of `count` tokens (4 ints each: slot, token, position, logits_row); logits rows 0..k-1 of
+// `vocabulary` floats. Returns the paged cache's status (0 on success).
+int orc_decoder_forward(void* handle, const int32_t* tokens, int count, float* logits, int threads) {
+    auto& m = *static_cast<DecoderOracle*>(handle);
+    const int status = orc_paged_step(m.cache, tokens, count);
+    if (status != 0) {
+        return status;
+    }
+    const int h = m.hidden;
+    const int kv = m.kv_heads * m.head_dim;
+    const int qkv_width = h + 2 * kv;
+    const int ffn = m.feed_forward;
+    std::vector<float> hidden(static_cast<size_t>(count) * h);
+    std::vector<float> normalized(hidden.size());
+    std::vector<float> qkv(static_cast<size_t>(count) * qkv_width);
+    std::vector<float> attention(hidden.size());
+    std::vector<float> gate_up(static_cast<size_t>(count) * 2 * ffn);
+    std::vector<float> activated(static_cast<size_t>(count) * ffn);
+    // synapse_embed_q8_0 (elementwise.cu:3-15).
+    const size_t row_bytes = static_cast<size_t>(h / 32) * 34;
+    for (int t = 0; t < count; ++t) {
+        const uint8_t* row = m.weights + m.token_embedding + static_cast<size_t>(tokens[4 * t + 1]) * row_bytes;
+        for (int c = 0; c < h; ++c) {
+            const uint8_t* block = row + static_cast<size_t>(c / 32) * 34;
+            hidden[static_cast<size_t>(t) * h + c] = q8_scale(block) * static_cast<float>(static_cast<int8_t>(block[2 + c % 32]));
+        }
+    }
+    for (int layer = 0; layer < m.layer_count; ++layer) {
+        const uint64_t* o = &m.layers[static_cast<size_t>(layer) * 15];
+        // attention_half (step/layers.rs:62-108).
+        for (int t = 0; t < count; ++t) {
+            rms_norm_row(&hidden[static_cast<size_t>(t) * h], f32_at(m, o[0]), h, m.epsilon,
+                         &normalized[static_cast<size_t>(t) * h]);
+        }
+        project_rows(m, o[1], o[4], h, h, count, normalized.data(), h, qkv.data(), qkv_width, 0, false, threads);
+        project_rows(m, o[2], o[5], kv, h, count, normalized.data(), h, qkv.data(), qkv_width, h, false, threads);
+        project_rows(m, o[3], o[6], kv, h, count, normalized.data(), h, qkv.data(), qkv_width, h + kv, false, threads);
+        const int appended = orc_paged_append_rope(m.cache, layer, qkv.data(), qkv_width, m.cosines.data(), m.sines.data());
+        if (appended != 0) {
+            return appended;
+        }
+        orc_paged_attention(m.cache, layer, qkv.data(), qkv_width, attention.data(), h, threads);
+        project_rows(m, o[9], kNoTensor, h, h, count, attention.data(), h, hidden.data(), h, 0, true, threads);
+        // feed_forward_half (step/layers.rs:150-206).
+        for (int t = 0; t < count; ++t) {
+            rms_norm_row(&hidden[static_cast<size_t>(t) * h], f32_at(m, o[10]), h, m.epsilon,
+                         &normalized[static_cast<size_t>(t) * h]);
+        }
+        project_rows(m, o[11], kNoTensor, ffn, h, count, normalized.data(), h, gate_up.data(), 2 * ffn, 0, false, threads);
+        project_rows(m, o[12], kNoTensor, ffn, h, count, normalized.data(), h, gate_up.data(), 2 * ffn, ffn, false,
+                     threads);
+        for (int t = 0; t < count; ++t) {
+            for (int c = 0; c < ffn; ++c) {
+                const float gate = gate_up[static_cast<size_t>(t) * 2 * ffn + c];
+                activated[static_cast<size_t>(t) * ffn + c] =
+                    gate / (1.0f + std::exp(-gate)) * gate_up[static_cast<size_t>(t) * 2 * ffn + ffn + c];
+            }
+        }
+        project_rows(m, o[13], kNoTensor, h, ffn, count, activated.data(), ffn, hidden.data(), h, 0, true, threads);
+    }
+    // logits (step/layers.rs:208-228): the gathered rows in token order.
+    int rows = 0;
+    for (int t = 0; t < count; ++t) {
+        if (tokens[4 * t + 3] >= 0) {
+            rms_norm_row(&hidden[static_cast<size_t>(t) * h], f32_at(m, m.output_norm), h, m.epsilon,
+                         &normalized[static_cast<size_t>(rows) * h]);
+            ++rows;
+        }
+    }
+    if (rows > 0) {
+        project_rows(m, m.output, kNoTensor, m.vocabulary, h, rows, normalized.data(), h, logits, m.vocabulary, 0, false,
+                     threads);
+    }
+    return 0;
+}
+
+}  // extern "C"

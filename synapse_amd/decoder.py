@@ -1,0 +1,225 @@
+"""The dense decoder step over libsynapse_kv (libsynapse_gpu's model API).
+
+``Decoder`` mirrors what the reference's managed executor does with a GPU model
+(src/Synapse.Runtime/Features/GpuKernels/GpuDecoderExecutor.cs; native/synapse-gpu/src/Features/GpuKernels/
+ffi.rs:106-271): it describes the mapped weights by byte offset (``DecoderDesc`` / ``DecoderLayerOffsets``,
+decoder.rs:60-116), hands over the RoPE tables, and runs batched steps of ``BatchToken`` rows that return the
+logits of the tokens that ask for them. There is no CPU fallback: without the HIP library every call raises.
+
+``synthetic_model`` writes a model file of a given shape with Q8_0 matrices and FP32 norms and biases (random
+values of sane magnitude, for tests and benchmarks; there is no network for real checkpoints).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from .kv_cache import batch_tokens, rope_table
+from .native import (
+    ALL_Q8_0,
+    ENCODING_Q8_0,
+    KV_F16,
+    KV_F32,
+    NO_TENSOR,
+    DecoderDesc,
+    LayerOffsets,
+    NativeKvLibrary,
+    PageActivation,
+    SELECT_KEY_BOUND,
+    SELECT_RANDOM,
+)
+
+BLOCK_ELEMENTS = 32
+BLOCK_BYTES = 34
+
+
+@dataclass
+class DecoderShape:
+    layers: int
+    hidden: int
+    feed_forward: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    vocabulary: int
+    context: int
+    session_slots: int = 4
+    step_tokens: int = 512
+    logits_rows: int = 16
+    rms_epsilon: float = 1e-6
+    kv_precision: str = "f32"
+    growth: int = 256
+    theta: float = 1_000_000.0
+
+    @property
+    def kv_width(self) -> int:
+        return self.kv_heads * self.head_dim
+
+
+def q8_bytes(rows: int, columns: int) -> int:
+    return rows * (columns // BLOCK_ELEMENTS) * BLOCK_BYTES
+
+
+def synthetic_model(shape: DecoderShape, seed: int = 0, biases: bool = True) -> tuple[np.ndarray, dict]:
+    """A model file: Q8_0 matrices (random codes, FP16 scales giving weights of standard deviation about
+    1/sqrt(columns)), FP32 norms near 1 and small FP32 biases. Returns (bytes, layout) where layout holds the byte
+    offsets in DecoderDesc / DecoderLayerOffsets terms."""
+    rng = np.random.default_rng(seed)
+    parts: list[tuple[str, int, object]] = []
+    offset = 0
+
+    def place(size: int, alignment: int) -> int:
+        nonlocal offset
+        offset = (offset + alignment - 1) // alignment * alignment
+        start = offset
+        offset += size
+        return start
+
+    def matrix(rows: int, columns: int, spread: float) -> int:
+        start = place(q8_bytes(rows, columns), 4)
+        parts.append(("q8", start, (rows, columns, spread)))
+        return start
+
+    def vector(values: int, center: float, spread: float) -> int:
+        start = place(values * 4, 4)
+        parts.append(("f32", start, (values, center, spread)))
+        return start
+
+    s = shape
+    layout = {"token_embedding": matrix(s.vocabulary, s.hidden, 1.0), "layers": []}
+    for _ in range(s.layers):
+        layer = {
+            "attention_norm": vector(s.hidden, 1.0, 0.2),
+            "query": matrix(s.hidden, s.hidden, s.hidden ** -0.5),
+            "key": matrix(s.kv_width, s.hidden, s.hidden ** -0.5),
+            "value": matrix(s.kv_width, s.hidden, s.hidden ** -0.5),
+            "query_bias": vector(s.hidden, 0.0, 0.1) if biases else NO_TENSOR,
+            "key_bias": vector(s.kv_width, 0.0, 0.1) if biases else NO_TENSOR,
+            "value_bias": vector(s.kv_width, 0.0, 0.1) if biases else NO_TENSOR,
+            "query_norm": NO_TENSOR,
+            "key_norm": NO_TENSOR,
+            "attention_output": matrix(s.hidden, s.hidden, s.hidden ** -0.5),
+            "feed_forward_norm": vector(s.hidden, 1.0, 0.2),
+            "gate": matrix(s.feed_forward, s.hidden, s.hidden ** -0.5),
+            "up": matrix(s.feed_forward, s.hidden, s.hidden ** -0.5),
+            "down": matrix(s.hidden, s.feed_forward, s.feed_forward ** -0.5),
+            "encodings": ALL_Q8_0,
+        }
+        layout["layers"].append(layer)
+    layout["output_norm"] = vector(s.hidden, 1.0, 0.2)
+    layout["output"] = matrix(s.vocabulary, s.hidden, s.hidden ** -0.5)
+    blob = np.zeros(offset, dtype=np.uint8)
+    for kind, start, spec in parts:
+        if kind == "f32":
+            values, center, spread = spec
+            data = (center + spread * (rng.random(values, dtype=np.float32) * 2 - 1)).astype(np.float32)
+            blob[start:start + values * 4] = data.view(np.uint8)
+        else:
+            rows, columns, spread = spec
+            blocks = rows * (columns // BLOCK_ELEMENTS)
+            view = blob[start:start + blocks * BLOCK_BYTES].reshape(blocks, BLOCK_BYTES)
+            view[:, 2:] = np.frombuffer(rng.bytes(blocks * BLOCK_ELEMENTS), dtype=np.uint8).reshape(blocks, 32)
+            # Uniform int8 codes have a standard deviation of about 74: scales around spread / 74, varied per block.
+            scales = (spread / 74.0) * (0.5 + rng.random(blocks, dtype=np.float32))
+            view[:, :2] = scales.astype(np.float16).view(np.uint8).reshape(blocks, 2)
+    return blob, layout
+
+
+class Decoder:
+    """A dense decoder on the device: ``forward(tokens)`` returns the logits rows the tokens ask for."""
+
+    def __init__(self, blob: np.ndarray, layout: dict, shape: DecoderShape, device: int = 0,
+                 library: NativeKvLibrary | None = None):
+        self.library = library or NativeKvLibrary.load()
+        self.shape = shape
+        self.blob = np.ascontiguousarray(blob, dtype=np.uint8)
+        self.cosines, self.sines = rope_table(shape.head_dim, shape.theta, shape.context, library=self.library)
+        self.layers = (LayerOffsets * shape.layers)()
+        for index, layer in enumerate(layout["layers"]):
+            for name, _ in LayerOffsets._fields_:
+                setattr(self.layers[index], name, int(layer[name]))
+        desc = DecoderDesc()
+        desc.weights = self.blob.ctypes.data
+        desc.weights_length = self.blob.nbytes
+        desc.layers = self.layers
+        desc.rope_cosines = self.cosines.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        desc.rope_sines = self.sines.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        desc.token_embedding = int(layout["token_embedding"])
+        desc.output_norm = int(layout["output_norm"])
+        desc.output = int(layout["output"])
+        desc.layer_count = shape.layers
+        desc.hidden = shape.hidden
+        desc.feed_forward = shape.feed_forward
+        desc.heads = shape.heads
+        desc.kv_heads = shape.kv_heads
+        desc.head_dim = shape.head_dim
+        desc.vocabulary = shape.vocabulary
+        desc.context = shape.context
+        desc.session_slots = shape.session_slots
+        desc.step_tokens = shape.step_tokens
+        desc.logits_rows = shape.logits_rows
+        desc.rms_epsilon = shape.rms_epsilon
+        desc.embedding_encoding = layout.get("embedding_encoding", ENCODING_Q8_0)
+        desc.rope_layout = layout.get("rope_layout", 0)
+        desc.activation = layout.get("activation", 0)
+        desc.kv_precision = KV_F16 if shape.kv_precision in ("f16", "fp16") else KV_F32
+        desc.kv_growth_positions = shape.growth
+        desc.output_encoding = layout.get("output_encoding", ENCODING_Q8_0)
+        self.desc = desc
+        handle = ctypes.c_void_p()
+        self.library.check(self.library.c_decoder_create(ctypes.byref(desc), device, ctypes.byref(handle)))
+        self.handle = handle
+        cache = ctypes.c_void_p()
+        self.library.check(self.library.c_decoder_cache(self.handle, ctypes.byref(cache)))
+        self.cache = cache
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.library.c_decoder_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream) -> None:
+        address = stream if isinstance(stream, int) else int(getattr(stream, "cuda_stream", 0) or 0)
+        self.library.check(self.library.c_decoder_set_stream(self.handle, address))
+
+    def reserve(self, slot: int, positions: int) -> None:
+        self.library.check(self.library.c_decoder_reserve(self.handle, slot, positions))
+
+    @property
+    def kv_bytes(self) -> int:
+        return int(self.library.c_decoder_kv_bytes(self.handle))
+
+    def forward(self, tokens, prompt_start: int | None = None) -> np.ndarray:
+        """One step of (slot, token, position, logits_row) rows; returns [k][vocabulary] FP32 logits."""
+        buffer = tokens if isinstance(tokens, ctypes.Array) else batch_tokens(tokens)
+        rows = sum(1 for token in buffer if token.logits_row >= 0)
+        logits = np.zeros((max(rows, 1), self.shape.vocabulary), dtype=np.float32)
+        if prompt_start is None:
+            status = self.library.c_decoder_forward(self.handle, buffer, len(buffer), logits.ctypes.data, logits.size)
+        else:
+            status = self.library.c_decoder_forward_prompt(self.handle, buffer, len(buffer), prompt_start,
+                                                           logits.ctypes.data, logits.size)
+        self.library.check(status)
+        return logits[:rows]
+
+    def set_option(self, option: int, value: int) -> None:
+        self.library.check(self.library.c_set_option(self.cache, option, value))
+
+    def set_page_activation(self, budget_pages: int | None, window_tokens: int = 0, selection: str = "key_bound",
+                            seed: int = 0) -> None:
+        """KV page activation on the model's cache (ModelLoadOptions.KvPageActivation); None: dense."""
+        if budget_pages is None:
+            activation = PageActivation(0, 0, 0, 64, SELECT_KEY_BOUND, 0)
+        else:
+            kind = {"key_bound": SELECT_KEY_BOUND, "random": SELECT_RANDOM}[selection]
+            activation = PageActivation(1, budget_pages, window_tokens, 64, kind, seed)
+        self.library.check(self.library.c_set_page_activation(self.cache, ctypes.byref(activation)))

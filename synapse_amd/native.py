@@ -158,13 +158,59 @@ class PageActivation(ctypes.Structure):
     ]
 
 
+NO_TENSOR = (1 << 64) - 1
+ENCODING_Q8_0 = 8
+ALL_Q8_0 = 0x08888888
+
+
+class LayerOffsets(ctypes.Structure):
+    """SynapseKvLayerOffsets: DecoderLayerOffsets (decoder.rs:60-81)."""
+
+    _fields_ = [(name, ctypes.c_uint64) for name in (
+        "attention_norm", "query", "key", "value", "query_bias", "key_bias", "value_bias", "query_norm", "key_norm",
+        "attention_output", "feed_forward_norm", "gate", "up", "down", "encodings")]
+
+
+class DecoderDesc(ctypes.Structure):
+    """SynapseKvDecoderDesc: DecoderDesc (decoder.rs:85-116)."""
+
+    _fields_ = [
+        ("weights", ctypes.c_void_p),
+        ("weights_length", ctypes.c_uint64),
+        ("layers", ctypes.POINTER(LayerOffsets)),
+        ("rope_cosines", ctypes.POINTER(ctypes.c_float)),
+        ("rope_sines", ctypes.POINTER(ctypes.c_float)),
+        ("token_embedding", ctypes.c_uint64),
+        ("output_norm", ctypes.c_uint64),
+        ("output", ctypes.c_uint64),
+        ("layer_count", ctypes.c_uint32),
+        ("hidden", ctypes.c_uint32),
+        ("feed_forward", ctypes.c_uint32),
+        ("heads", ctypes.c_uint32),
+        ("kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("vocabulary", ctypes.c_uint32),
+        ("context", ctypes.c_uint32),
+        ("session_slots", ctypes.c_uint32),
+        ("step_tokens", ctypes.c_uint32),
+        ("logits_rows", ctypes.c_uint32),
+        ("rms_epsilon", ctypes.c_float),
+        ("embedding_encoding", ctypes.c_uint32),
+        ("rope_layout", ctypes.c_uint32),
+        ("activation", ctypes.c_uint32),
+        ("kv_precision", ctypes.c_uint32),
+        ("kv_growth_positions", ctypes.c_uint32),
+        ("output_encoding", ctypes.c_uint32),
+    ]
+
+
 class Profile(ctypes.Structure):
     _fields_ = [("launches", ctypes.c_uint64 * 8), ("milliseconds", ctypes.c_double * 8)]
 
 
 # Sizes pinned on both sides of the ABI (include/synapse_kv.h static assertions).
 STRUCT_SIZES = {DeviceInfo: 152, BatchToken: 16, CacheDesc: 64, PageStats: 40, Profile: 128, Matrix: 24,
-                Projection: 48, PageActivation: 24}
+                Projection: 48, PageActivation: 24, LayerOffsets: 120, DecoderDesc: 136}
 for _struct, _size in STRUCT_SIZES.items():
     assert ctypes.sizeof(_struct) == _size, (_struct.__name__, ctypes.sizeof(_struct))
 
@@ -213,6 +259,14 @@ EXPORTS = {
     "synapse_kv_weights_set_stream": (_I32, [_P, _P]),
     "synapse_kv_project": (_I32, [_P, ctypes.POINTER(Projection), _P, _P]),
     "synapse_kv_weights_read": (_I32, [_P, _U32, _P, _U64]),
+    "synapse_kv_decoder_create": (_I32, [ctypes.POINTER(DecoderDesc), _I32, ctypes.POINTER(_P)]),
+    "synapse_kv_decoder_forward": (_I32, [_P, ctypes.POINTER(BatchToken), _SIZE, _P, _SIZE]),
+    "synapse_kv_decoder_forward_prompt": (_I32, [_P, ctypes.POINTER(BatchToken), _SIZE, _SIZE, _P, _SIZE]),
+    "synapse_kv_decoder_destroy": (None, [_P]),
+    "synapse_kv_decoder_kv_bytes": (_U64, [_P]),
+    "synapse_kv_decoder_reserve": (_I32, [_P, _U32, _U32]),
+    "synapse_kv_decoder_cache": (_I32, [_P, ctypes.POINTER(_P)]),
+    "synapse_kv_decoder_set_stream": (_I32, [_P, _P]),
 }
 
 

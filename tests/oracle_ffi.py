@@ -52,6 +52,10 @@ SIGNATURES = {
     "orc_dotnet_random": (None, [ctypes.c_int32, _I, ctypes.c_int32, ctypes.c_int32, _P]),
     "orc_page_bound": (_F, [_P, _I, _I, _P, _I, _I]),
     "orc_page_select": (None, [_I, _I, _I, _I, _P, _I, _I, _P, _I, ctypes.c_int32, _P]),
+    "orc_decoder_create": (_P, [_P, _P, _P, _P, _F, _P, _P]),
+    "orc_decoder_destroy": (None, [_P]),
+    "orc_decoder_cache": (_P, [_P]),
+    "orc_decoder_forward": (_I, [_P, _P, _I, _P, _I]),
     "orc_plan_attention": (_I, [_P, _I, _I, _I, _P, _I, _P]),
     "orc_prefix_create": (_P, [_I]),
     "orc_prefix_destroy": (None, [_P]),
@@ -338,3 +342,40 @@ def page_select(budget, window, queries, group, head_dim, keys, position, seed=0
     ORACLE.orc_page_select(budget, window, page_tokens, 1 if random else 0, ptr(q), group, head_dim, ptr(k), position,
                            seed, ptr(selected))
     return selected.astype(bool)
+
+
+LAYER_FIELDS = ("attention_norm", "query", "key", "value", "query_bias", "key_bias", "value_bias", "query_norm",
+                "key_norm", "attention_output", "feed_forward_norm", "gate", "up", "down", "encodings")
+
+
+class DecoderOracle:
+    """The decoder step restated on the CPU (orc_decoder_*), over a model file and its layout."""
+
+    def __init__(self, blob, layout, shape, cosines, sines, page_tokens=64, max_pages=None):
+        self.blob = np.ascontiguousarray(blob, dtype=np.uint8)
+        self.shape = shape
+        self.cosines = np.ascontiguousarray(cosines, dtype=np.float32)
+        self.sines = np.ascontiguousarray(sines, dtype=np.float32)
+        self.layers = np.array([[int(layer[name]) for name in LAYER_FIELDS] for layer in layout["layers"]],
+                               dtype=np.uint64)
+        self.top = np.array([layout["token_embedding"], layout["output_norm"], layout["output"]], dtype=np.uint64)
+        pages = max_pages or shape.session_slots * -(-shape.context // page_tokens)
+        precision = 1 if shape.kv_precision in ("f16", "fp16") else 0
+        self.dims = np.array([shape.layers, shape.hidden, shape.feed_forward, shape.heads, shape.kv_heads,
+                              shape.head_dim, shape.vocabulary, shape.context, shape.session_slots, shape.step_tokens,
+                              precision, shape.growth, page_tokens, pages], dtype=np.int32)
+        self.handle = ORACLE.orc_decoder_create(ptr(self.blob), ptr(self.layers), ptr(self.top), ptr(self.dims),
+                                                shape.rms_epsilon, ptr(self.cosines), ptr(self.sines))
+        assert self.handle
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            ORACLE.orc_decoder_destroy(self.handle)
+
+    def forward(self, tokens, threads=8):
+        array = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1, 4)
+        rows = int((array[:, 3] >= 0).sum())
+        logits = np.zeros((max(rows, 1), self.shape.vocabulary), dtype=np.float32)
+        status = ORACLE.orc_decoder_forward(self.handle, ptr(array), array.shape[0], ptr(logits), threads)
+        assert status == 0, status
+        return logits[:rows]

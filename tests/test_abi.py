@@ -139,3 +139,68 @@ def test_weights_create_validates_before_the_device(native, rows, columns, weigh
                                    ctypes.byref(handle)) == 2
     assert "invalid argument" in native.last_error()
     assert not handle.value
+
+
+def decoder_desc(**overrides):
+    """A valid SynapseKvDecoderDesc over a tiny synthetic model file, with fields overridden."""
+    from synapse_amd.decoder import DecoderShape, synthetic_model
+    from synapse_amd.native import DecoderDesc, LayerOffsets
+
+    shape = DecoderShape(layers=1, hidden=128, feed_forward=256, heads=2, kv_heads=1, head_dim=64, vocabulary=64,
+                         context=128, session_slots=2, step_tokens=8, logits_rows=4, growth=64)
+    blob, layout = synthetic_model(shape, seed=1)
+    layer_overrides = overrides.pop("layer", {})
+    layers = (LayerOffsets * 1)()
+    for name, _ in LayerOffsets._fields_:
+        setattr(layers[0], name, int(layer_overrides.get(name, layout["layers"][0][name])))
+    cos = np.zeros((128, 32), dtype=np.float32)
+    desc = DecoderDesc()
+    desc.weights = blob.ctypes.data
+    desc.weights_length = blob.nbytes
+    desc.layers = layers
+    desc.rope_cosines = cos.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    desc.rope_sines = cos.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    fields = dict(token_embedding=layout["token_embedding"], output_norm=layout["output_norm"],
+                  output=layout["output"], layer_count=1, hidden=128, feed_forward=256, heads=2, kv_heads=1,
+                  head_dim=64, vocabulary=64, context=128, session_slots=2, step_tokens=8, logits_rows=4,
+                  rms_epsilon=1e-6, embedding_encoding=8, rope_layout=0, activation=0, kv_precision=0,
+                  kv_growth_positions=64, output_encoding=8)
+    fields.update(overrides)
+    for name, value in fields.items():
+        setattr(desc, name, value)
+    return desc, (blob, layers, cos)
+
+
+@pytest.mark.parametrize("overrides,status,message", [
+    ({"output_encoding": 12}, 3, "K-quant"),
+    ({"embedding_encoding": 2}, 3, "not GGML type 2"),
+    ({"rope_layout": 2}, 3, "NeoX RoPE"),
+    ({"activation": 1}, 3, "SwiGLU"),
+    ({"head_dim": 96, "hidden": 192}, 3, "head dimensions"),
+    ({"heads": 18, "kv_heads": 2, "hidden": 18 * 64}, 3, "at most 8"),
+    ({"rms_epsilon": 0.0}, 2, "epsilon"),
+    ({"kv_growth_positions": 32}, 2, "multiple of 64"),
+    ({"feed_forward": 0}, 2, "positive"),
+    ({"output": 10**9}, 2, "tensor output"),
+    ({"output_norm": 2}, 2, "tensor output_norm"),
+    ({"layer": {"query_norm": 0}}, 3, "query/key normalization"),
+    ({"layer": {"encodings": 0x08888C88}}, 3, "K-quant"),
+    ({"layer": {"key_bias": 10**9}}, 2, "layer 0: tensor attn_k.bias"),
+    ({"layer": {"gate": 1}}, 2, "layer 0: tensor ffn_gate"),
+])
+def test_decoder_create_validates_the_description_first(native, overrides, status, message):
+    # DecoderPlan::new (decoder.rs:246-294, checks.rs) runs before any device work.
+    desc, _keep = decoder_desc(**overrides)
+    handle = ctypes.c_void_p()
+    assert native.c_decoder_create(ctypes.byref(desc), 0, ctypes.byref(handle)) == status
+    assert message in native.last_error()
+    assert not handle.value
+
+
+def test_decoder_null_pointers(native):
+    assert native.c_decoder_create(None, 0, None) == 1
+    assert native.c_decoder_forward(None, None, 0, None, 0) == 1
+    assert native.c_decoder_reserve(None, 0, 0) == 1
+    assert native.c_decoder_kv_bytes(None) == 0
+    assert native.c_decoder_cache(None, None) == 1
+    native.c_decoder_destroy(None)
