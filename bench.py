@@ -568,12 +568,97 @@ def config_projection(args, torch) -> dict:
     return line
 
 
+def config_decoder(args, torch) -> dict:
+    """The whole decoder step (synapse_kv_decoder_forward) on a Qwen2.5-7B-shaped synthetic Q8_0 model: 16
+    sequences at the C3 lengths decode one token each per step, every token's logits copied back. The KV cache is
+    filled through the model's cache (random K/V rows, as C3) rather than by running the prompts, which would
+    only take longer. Algorithmic bytes per step: every Q8_0 matrix once (QKV, O, gate, up, down, logits), the K/V
+    of every attended position, the new K/V, the embedding rows and the logits written."""
+    import ctypes
+
+    from synapse_amd.decoder import Decoder, DecoderShape, q8_bytes, synthetic_model
+    from synapse_amd.kv_cache import batch_tokens
+
+    lengths = lengths_for(SEED + CONFIG_OFFSET)
+    total = args.warmup + args.steps
+    context = int(-(-(int(lengths.max()) + total + 1) // GROWTH) * GROWTH)
+    shape = DecoderShape(layers=LAYERS, hidden=HEADS * HEAD_DIM, feed_forward=18944, heads=HEADS, kv_heads=KV_HEADS,
+                         head_dim=HEAD_DIM, vocabulary=152064, context=context, session_slots=SEQUENCES,
+                         step_tokens=4096, logits_rows=SEQUENCES, kv_precision="f16", growth=GROWTH)
+    started = time.perf_counter()
+    blob, layout = synthetic_model(shape, seed=SEED + 8)
+    model = Decoder(blob, layout, shape)
+    log(f"model {blob.nbytes / 2**30:.2f} GiB built and uploaded in {time.perf_counter() - started:.1f} s")
+    library = model.library
+    cache = model.cache
+    generator = torch.Generator(device="cuda")
+    generator.manual_seed(SEED + 8)
+    width = (HEADS + 2 * KV_HEADS) * HEAD_DIM
+    chunk = 4096
+    rows = torch.empty((chunk, width), device="cuda")
+    for slot, length in enumerate(lengths.tolist()):
+        library.check(library.c_reserve(cache, slot, length + total + 1))
+        for first in range(0, length, chunk):
+            count = min(chunk, length - first)
+            tokens = batch_tokens([(slot, p) for p in range(first, first + count)])
+            library.check(library.c_step(cache, tokens, count))
+            for layer in range(LAYERS):
+                rows[:count].normal_(generator=generator)
+                library.check(library.c_append_rope(cache, layer, rows.data_ptr(), width))
+    torch.cuda.synchronize()
+    log(f"KV filled: {model.kv_bytes / 2**30:.2f} GiB")
+    rng = np.random.default_rng(SEED + 8)
+    # The logits land in a reused pinned host buffer (the caller's buffer; a fresh pageable array per step would
+    # time page faults and a staged copy).
+    pinned = torch.empty((SEQUENCES, shape.vocabulary), dtype=torch.float32, pin_memory=True).numpy()
+
+    def step(index):
+        return model.forward([(slot, int(rng.integers(shape.vocabulary)), int(lengths[slot]) + index, slot)
+                              for slot in range(SEQUENCES)], out=pinned)
+
+    for index in range(args.warmup):
+        step(index)
+    torch.cuda.synchronize()
+    begin = time.perf_counter()
+    for index in range(args.steps):
+        logits = step(args.warmup + index)
+    elapsed = time.perf_counter() - begin
+    assert np.isfinite(logits).all()
+    seconds = elapsed / args.steps
+    s = shape
+    kv = s.kv_width
+    weight_bytes = s.layers * (q8_bytes(s.hidden + 2 * kv, s.hidden) + q8_bytes(s.hidden, s.hidden) +
+                               2 * q8_bytes(s.feed_forward, s.hidden) + q8_bytes(s.hidden, s.feed_forward)) + \
+        q8_bytes(s.vocabulary, s.hidden)
+    keys = float(np.mean([(lengths + args.warmup + i + 1).sum() for i in range(args.steps)]))
+    kv_bytes = keys * KV_BYTES_PER_TOKEN_LAYER * LAYERS + SEQUENCES * KV_BYTES_PER_TOKEN_LAYER * LAYERS
+    other = SEQUENCES * (q8_bytes(1, s.hidden) + s.vocabulary * 4)
+    step_bytes = weight_bytes + kv_bytes + other
+    model.close()
+    achieved = step_bytes / seconds / 1e9
+    return {
+        "metric": "decoder step tokens/s (embedding, 28 layers, logits), 7B-shaped Q8_0, 16 sequences @ C3 lengths",
+        "value": round(SEQUENCES / seconds, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(seconds * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 (Q8_0 weights, FP16 KV)",
+        "data": f"synthetic Q8_0 model (numpy seed {SEED + 8}), random K/V prefill, random token ids",
+        "config": {"workload": "decoder: Qwen2.5-7B shape (hidden 3,584, ffn 18,944, 28 q / 4 KV heads, vocab "
+                               "152,064), 16 sequences decoding at lengths U[1024, 32768], logits for every token",
+                   "layers": LAYERS, "lengths": lengths.tolist(), "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "whole step (all kernels)", "achieved": round(achieved, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
+                     "traffic": None, "algorithmic_bytes_per_step": int(step_bytes),
+                     "weight_bytes": int(weight_bytes), "kv_bytes": int(kv_bytes)},
+    }
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5", "proj"], default="c3",
+    parser.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5", "proj", "decoder"], default="c3",
                         help="c3: the BASELINE metric (default); c1, c2, c4: the other decode configurations; "
-                             "c5: chunked-prefill MFMA throughput; proj: the Q8_0 projections around the path")
+                             "c5: chunked-prefill MFMA throughput; proj: the Q8_0 projections around the path; "
+                             "decoder: the whole decoder step on a 7B-shaped synthetic model")
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--split-keys", type=int, default=None)
@@ -601,7 +686,7 @@ def main() -> None:
     torch.cuda.set_device(0)
     if args.config != "c3":
         runner = {"c1": config_c1, "c2": config_c2, "c4": config_c4, "c5": prefill_config,
-                  "proj": config_projection}[args.config]
+                  "proj": config_projection, "decoder": config_decoder}[args.config]
         print(json.dumps(runner(args, torch)), flush=True)
         return
     lengths = lengths_for(SEED + CONFIG_OFFSET)

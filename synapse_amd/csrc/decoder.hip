@@ -47,18 +47,34 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* table, uint32
 }
 
 // synapse_rms_norm (elementwise.cu:17-52): y = x * (1 / sqrt(mean(x^2) + eps)) * w, one workgroup per row; with
-// `gather` row r reads input row gather[r] (the logits rows). The sum of squares is reduced per wave, then across
-// the workgroup's waves in order.
+// `gather` row r reads input row gather[r] (the logits rows). Each thread keeps its columns (16-byte groups, up to
+// kNormGroups of them, i.e. hidden <= 8,192) in registers: all loads are issued before the sum, and the row is read
+// once. The sum of squares is reduced per wave, then across the workgroup's waves in order.
+constexpr int kNormGroups = 8;
 #pragma clang fp contract(off)
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* input, const int32_t* gather, const float* weight,
                                                        uint32_t columns, float epsilon, float* output) {
     __shared__ float partial[4];
     const int row = blockIdx.x;
     const size_t source = gather != nullptr ? static_cast<size_t>(gather[row]) : static_cast<size_t>(row);
-    const float* x = input + source * columns;
+    const float4* x = reinterpret_cast<const float4*>(input + source * columns);
+    const float4* w = reinterpret_cast<const float4*>(weight);
+    const uint32_t groups = columns / 4;
+    float4 values[kNormGroups];
+    float4 scales[kNormGroups];
+#pragma unroll
+    for (int j = 0; j < kNormGroups; ++j) {
+        const uint32_t index = threadIdx.x + 256 * j;
+        values[j] = index < groups ? x[index] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        scales[j] = index < groups ? w[index] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     float sum = 0.0f;
-    for (uint32_t i = threadIdx.x; i < columns; i += blockDim.x) {
-        sum += x[i] * x[i];
+#pragma unroll
+    for (int j = 0; j < kNormGroups; ++j) {
+        sum += values[j].x * values[j].x;
+        sum += values[j].y * values[j].y;
+        sum += values[j].z * values[j].z;
+        sum += values[j].w * values[j].w;
     }
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
@@ -70,9 +86,15 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* input, const
     __syncthreads();
     const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
     const float scale = 1.0f / sqrtf(total / static_cast<float>(columns) + epsilon);
-    float* y = output + static_cast<size_t>(row) * columns;
-    for (uint32_t i = threadIdx.x; i < columns; i += blockDim.x) {
-        y[i] = x[i] * scale * weight[i];
+    float4* y = reinterpret_cast<float4*>(output + static_cast<size_t>(row) * columns);
+#pragma unroll
+    for (int j = 0; j < kNormGroups; ++j) {
+        const uint32_t index = threadIdx.x + 256 * j;
+        if (index < groups) {
+            const float4 v = values[j];
+            const float4 s = scales[j];
+            y[index] = make_float4(v.x * scale * s.x, v.y * scale * s.y, v.z * scale * s.z, v.w * scale * s.w);
+        }
     }
 }
 
@@ -236,6 +258,11 @@ void validate(const SynapseKvDecoderDesc& d) {
     }
     if (d.hidden % 32 != 0 || d.feed_forward % 32 != 0) {
         invalid("hidden and feed-forward widths must be multiples of 32");
+    }
+    if (d.hidden > 4 * 256 * kNormGroups) {
+        fail(SYNAPSE_KV_UNAVAILABLE, "the RMS norm kernel keeps a row in registers: hidden widths up to " +
+                                         std::to_string(4 * 256 * kNormGroups) + " (the model has " +
+                                         std::to_string(d.hidden) + ")");
     }
     if (d.kv_precision != SYNAPSE_KV_F32 && d.kv_precision != SYNAPSE_KV_F16) {
         invalid("unknown KV precision " + std::to_string(d.kv_precision));

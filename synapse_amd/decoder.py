@@ -198,11 +198,17 @@ class Decoder:
     def kv_bytes(self) -> int:
         return int(self.library.c_decoder_kv_bytes(self.handle))
 
-    def forward(self, tokens, prompt_start: int | None = None) -> np.ndarray:
-        """One step of (slot, token, position, logits_row) rows; returns [k][vocabulary] FP32 logits."""
+    def forward(self, tokens, prompt_start: int | None = None, out: np.ndarray | None = None) -> np.ndarray:
+        """One step of (slot, token, position, logits_row) rows; returns [k][vocabulary] FP32 logits, written into
+        `out` when given (a reusable, ideally pinned, host buffer of at least k rows)."""
         buffer = tokens if isinstance(tokens, ctypes.Array) else batch_tokens(tokens)
         rows = sum(1 for token in buffer if token.logits_row >= 0)
-        logits = np.zeros((max(rows, 1), self.shape.vocabulary), dtype=np.float32)
+        if out is not None:
+            if out.dtype != np.float32 or not out.flags["C_CONTIGUOUS"] or out.size < rows * self.shape.vocabulary:
+                raise ValueError("out must be a contiguous float32 buffer of at least k x vocabulary values")
+            logits = out.reshape(-1)[:max(rows, 1) * self.shape.vocabulary].reshape(max(rows, 1), -1)
+        else:
+            logits = np.zeros((max(rows, 1), self.shape.vocabulary), dtype=np.float32)
         if prompt_start is None:
             status = self.library.c_decoder_forward(self.handle, buffer, len(buffer), logits.ctypes.data, logits.size)
         else:
