@@ -412,9 +412,23 @@ __global__ __launch_bounds__(256) void reduce_kernel(ProjectionArgs a) {
         return;
     }
     const float* partial = a.partials + static_cast<size_t>(t) * a.partial_stride + global_row;
+    const size_t stride = static_cast<size_t>(16) * a.partial_stride;
+    // Slices summed in order; eight loads in flight at a time.
     float sum = partial[0];
-    for (int slice = 1; slice < a.slices; ++slice) {
-        sum += partial[static_cast<size_t>(slice) * 16 * a.partial_stride];
+    int slice = 1;
+    for (; slice + 8 <= a.slices; slice += 8) {
+        float values[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            values[i] = partial[(slice + i) * stride];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sum += values[i];
+        }
+    }
+    for (; slice < a.slices; ++slice) {
+        sum += partial[slice * stride];
     }
     const float total = sum + (seg.bias != nullptr ? seg.bias[row] : 0.0f);
     float* destination = a.output + static_cast<size_t>(t) * a.out_stride + seg.out_column + row;
