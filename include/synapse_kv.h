@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 /* ABI version checked by the loader before any other call (ffi.rs:12 ABI_VERSION; NativeGpuLibrary.cs:14). */
-#define SYNAPSE_KV_ABI_VERSION 3u
+#define SYNAPSE_KV_ABI_VERSION 4u
 
 /* Status codes, identical to error.rs:4-16. */
 #define SYNAPSE_KV_OK 0
@@ -269,6 +269,14 @@ typedef struct SynapseKvWeights SynapseKvWeights;
 int32_t synapse_kv_weights_create(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMatrix* matrices,
                                   uint32_t count, SynapseKvWeights** weights);
 
+/* The same for matrices in other GGML encodings (ADR-021; decoder/encoding.rs:5-73): encodings[i] is matrix i's
+ * GGML type id, SYNAPSE_KV_ENCODING_Q8_0 (8), SYNAPSE_KV_ENCODING_Q4_K (12; 144-byte super-blocks of 256 values) or
+ * SYNAPSE_KV_ENCODING_Q6_K (14; 210 bytes per 256 values); null means all Q8_0. K-quant matrices need columns that
+ * are a multiple of 256 and keep 4-bit (Q4_K) or 8-bit (Q6_K) codes on the device with FP32 per-block factors;
+ * other ids are SYNAPSE_KV_UNAVAILABLE. The segments of one projection may mix encodings. */
+int32_t synapse_kv_weights_create_encoded(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMatrix* matrices,
+                                          const uint32_t* encodings, uint32_t count, SynapseKvWeights** weights);
+
 /* Null is ignored. */
 void synapse_kv_weights_destroy(SynapseKvWeights* weights);
 
@@ -300,7 +308,7 @@ int32_t synapse_kv_project(SynapseKvWeights* weights, const SynapseKvProjection*
                            float* output);
 
 /* Copies matrix `index` back in GGML Q8_0 block order (rows x columns / 32 blocks of 34 bytes) into host memory of
- * at least that many bytes (read-back for checks). */
+ * at least that many bytes (read-back for checks); K-quant matrices are SYNAPSE_KV_UNAVAILABLE. */
 int32_t synapse_kv_weights_read(SynapseKvWeights* weights, uint32_t index, uint8_t* blocks, uint64_t bytes);
 
 /* ---- The dense decoder step (libsynapse_gpu's model API, ffi.rs:106-271; decoder.rs:60-136) ----
@@ -311,7 +319,9 @@ int32_t synapse_kv_weights_read(SynapseKvWeights* weights, uint32_t index, uint8
  * cache and one weights handle, on one stream. */
 
 #define SYNAPSE_KV_NO_TENSOR 0xFFFFFFFFFFFFFFFFull /* NO_TENSOR: an optional tensor the model does not have */
-#define SYNAPSE_KV_ENCODING_Q8_0 8u               /* GGML type IDs (ADR-021); Q4_K (12) and Q6_K (14) are UNAVAILABLE */
+#define SYNAPSE_KV_ENCODING_Q8_0 8u               /* GGML type IDs (ADR-021, decoder/encoding.rs:5-10) */
+#define SYNAPSE_KV_ENCODING_Q4_K 12u
+#define SYNAPSE_KV_ENCODING_Q6_K 14u
 #define SYNAPSE_KV_ALL_Q8_0 0x08888888ull         /* DecoderLayerOffsets.encodings with every matrix in Q8_0 */
 #define SYNAPSE_KV_ROPE_NEOX 0u
 #define SYNAPSE_KV_ACTIVATION_SWIGLU 0u
@@ -371,7 +381,8 @@ typedef struct SynapseKvDecoder SynapseKvDecoder;
 
 /* synapse_gpu_decoder_create (ffi.rs:106-137) with DecoderPlan::new's validation (decoder/checks.rs): status 2
  * for inconsistent shapes and out-of-range or misaligned tensors, 3 for what the kernels do not implement
- * (encodings other than Q8_0, RoPE layouts other than NeoX, activations other than SwiGLU, per-head Q/K norms,
+ * (encodings other than Q8_0, Q4_K and Q6_K, K-quant matrices whose columns are not whole 256-value super-blocks,
+ * RoPE layouts other than NeoX, activations other than SwiGLU, per-head Q/K norms,
  * head dimensions other than 64 and 128, more than 8 query heads per KV head). Uploads the matrices (repacked), the
  * norms, biases and the embedding table to device memory on `device`; the KV page pool takes the pages every slot
  * needs at full context, or what fits in free device memory. */

@@ -1579,6 +1579,7 @@ struct DecoderOracle {
     const uint8_t* weights;
     std::vector<uint64_t> layers;  // layer_count x 15 offsets (DecoderLayerOffsets order)
     uint64_t token_embedding, output_norm, output;
+    int embedding_encoding, output_encoding;
     int layer_count, hidden, feed_forward, heads, kv_heads, head_dim, vocabulary;
     float epsilon;
     std::vector<float> cosines, sines;
@@ -1603,18 +1604,133 @@ void rms_norm_row(const float* x, const float* w, int columns, float epsilon, fl
     }
 }
 
-// Rows of one Q8_0 matrix (rows x columns at `offset`) times input rows, plus an optional FP32 bias, into
-// output[t * out_stride + out_column + row] (added to it when accumulating).
-void project_rows(const DecoderOracle& m, uint64_t offset, uint64_t bias, int rows, int columns, int tokens,
-                  const float* input, int in_stride, float* output, int out_stride, int out_column, bool accumulate,
-                  int threads) {
+// ---- K-quant matrices (ADR-021) ----
+// GGML Q4_K: 144-byte super-blocks of 256 values (FP16 d, FP16 dmin, 12 packed 6-bit scale/minimum bytes, 128 bytes
+// of nibbles); Q6_K: 210 bytes (ql[128], qh[64], int8 scales[16], FP16 d). GgufKQuantBlocks.cs:99-177 and
+// matmul_kquant.metal:16-68 decode them; the functions below restate that decoding.
+constexpr int kQ4K = 12;
+constexpr int kQ6K = 14;
+
+int kq_block_bytes(int encoding) { return encoding == kQ4K ? 144 : 210; }
+
+float f16_at(const uint8_t* p) {
+    uint16_t bits;
+    std::memcpy(&bits, p, 2);
+    return f16_to_f32(bits);
+}
+
+// Code of value i of a super-block: Q4_K q (0..15); Q6_K q - 32 (ScaleMinK4 :149-153, DecodeQ6K :155-177).
+int kq_code(int encoding, const uint8_t* block, int i) {
+    const int sub = i / 32;
+    const int l = i % 32;
+    if (encoding == kQ4K) {
+        const uint8_t byte = block[16 + (sub / 2) * 32 + l];
+        return sub % 2 == 0 ? (byte & 0xF) : (byte >> 4);
+    }
+    const int half = sub / 4;
+    const int quarter = sub % 4;
+    const uint8_t low = block[half * 64 + (quarter % 2 == 0 ? l : l + 32)];
+    const int nibble = quarter < 2 ? (low & 0xF) : (low >> 4);
+    const int high = (block[128 + half * 32 + l] >> (2 * quarter)) & 3;
+    return (nibble | (high << 4)) - 32;
+}
+
+// The factors of value i: Q4_K scale d * sc_j and offset dmin * m_j of sub-block j = i / 32; Q6_K scale
+// d * scales[i / 16] and offset 0 (kq_decode8, matmul_kquant.metal:76-113).
+void kq_factors(int encoding, const uint8_t* block, int i, float& scale, float& offset) {
+    if (encoding == kQ4K) {
+        const int j = i / 32;
+        const uint8_t* packed = block + 4;
+        int sc;
+        int mn;
+        if (j < 4) {
+            sc = packed[j] & 63;
+            mn = packed[j + 4] & 63;
+        } else {
+            sc = (packed[j + 4] & 0xF) | ((packed[j - 4] >> 6) << 4);
+            mn = (packed[j + 4] >> 4) | ((packed[j] >> 6) << 4);
+        }
+        scale = f16_at(block) * static_cast<float>(sc);
+        offset = f16_at(block + 2) * static_cast<float>(mn);
+    } else {
+        scale = f16_at(block + 208) * static_cast<float>(static_cast<int8_t>(block[192 + i / 16]));
+        offset = 0.0f;
+    }
+}
+
+// One value of a K-quant row (kq_values8: d1 * q - m1, scale * (q - 32)).
+float kq_value(int encoding, const uint8_t* row, int column) {
+    const uint8_t* block = row + static_cast<size_t>(column / 256) * kq_block_bytes(encoding);
+    float scale;
+    float offset;
+    kq_factors(encoding, block, column % 256, scale, offset);
+    const float q = static_cast<float>(kq_code(encoding, block, column % 256));
+    return encoding == kQ4K ? scale * q - offset : scale * q;
+}
+
+// synapse_kq_matvec (matmul_kquant.metal:153-210) for one (row, token): 32 lanes; lane (slot = l / 4, quarter =
+// l % 4) walks 32-value chunks slot, slot + 8, ... and adds kq_apply = scale * (q0.x0 + q1.x1) - offset * (sum x0 +
+// sum x1) for its 8 values; the lanes are added in a butterfly (simd_sum; restated in the xor-shuffle order).
+float kq_matvec_row(int encoding, const uint8_t* row, int columns, const float* x) {
+    float lane[32];
+    for (int l = 0; l < 32; ++l) {
+        const int slot = l / 4;
+        const int quarter = l % 4;
+        float sum = 0.0f;
+        for (int chunk = slot; chunk < columns / 32; chunk += 8) {
+            const uint8_t* block = row + static_cast<size_t>(chunk / 8) * kq_block_bytes(encoding);
+            const int first = (chunk % 8) * 32 + quarter * 8;
+            float scale;
+            float offset;
+            kq_factors(encoding, block, first, scale, offset);
+            const float* v = x + chunk * 32 + quarter * 8;
+            float dots[2];
+            float sums[2];
+            for (int h = 0; h < 2; ++h) {
+                const float* q4 = v + 4 * h;
+                float qv[4];
+                for (int i = 0; i < 4; ++i) {
+                    qv[i] = static_cast<float>(kq_code(encoding, block, first + 4 * h + i));
+                }
+                dots[h] = ((qv[0] * q4[0] + qv[1] * q4[1]) + qv[2] * q4[2]) + qv[3] * q4[3];
+                sums[h] = ((q4[0] + q4[1]) + q4[2]) + q4[3];
+            }
+            const float qx = dots[0] + dots[1];
+            const float sx = sums[0] + sums[1];
+            sum += scale * qx - offset * sx;
+        }
+        lane[l] = sum;
+    }
+    for (int offset = 16; offset > 0; offset >>= 1) {
+        float next[32];
+        for (int l = 0; l < 32; ++l) {
+            next[l] = lane[l] + lane[l ^ offset];
+        }
+        std::memcpy(lane, next, sizeof(lane));
+    }
+    return lane[0];
+}
+
+// Bytes of one row of a matrix in `encoding` (8: Q8_0, 12: Q4_K, 14: Q6_K).
+size_t row_bytes_of(int encoding, int columns) {
+    return encoding == 8 ? static_cast<size_t>(columns / 32) * 34
+                         : static_cast<size_t>(columns / 256) * kq_block_bytes(encoding);
+}
+
+// Rows of one matrix (rows x columns at `offset`, GGML blocks of `encoding`) times input rows, plus an optional
+// FP32 bias, into output[t * out_stride + out_column + row] (added to it when accumulating). Q8_0 follows
+// matmul.cu's order, the K-quants matmul_kquant.metal's.
+void project_rows(const DecoderOracle& m, uint64_t offset, uint64_t bias, int encoding, int rows, int columns,
+                  int tokens, const float* input, int in_stride, float* output, int out_stride, int out_column,
+                  bool accumulate, int threads) {
     const int blocks = columns / 32;
-    const size_t row_bytes = static_cast<size_t>(blocks) * 34;
+    const size_t row_bytes = row_bytes_of(encoding, columns);
     const float* biases = bias == kNoTensor ? nullptr : f32_at(m, bias);
     Pool::run(rows, threads, [&](int, int row) {
         const uint8_t* weights = m.weights + offset + row * row_bytes;
         for (int t = 0; t < tokens; ++t) {
-            float total = q8_matvec_row(weights, blocks, input + static_cast<size_t>(t) * in_stride);
+            const float* x = input + static_cast<size_t>(t) * in_stride;
+            float total = encoding == 8 ? q8_matvec_row(weights, blocks, x) : kq_matvec_row(encoding, weights, columns, x);
             if (biases != nullptr) {
                 total += biases[row];
             }
@@ -1630,7 +1746,8 @@ extern "C" {
 
 // dims: layer_count, hidden, feed_forward, heads, kv_heads, head_dim, vocabulary, context, session_slots,
 // step_tokens, kv_precision, kv_growth_positions, page_tokens, max_pages. top: token_embedding, output_norm,
-// output. layers: layer_count x 15 offsets. The weights stay owned by the caller.
+// output, embedding_encoding, output_encoding. layers: layer_count x 15 values (DecoderLayerOffsets: 14 offsets,
+// then the packed encodings). The weights stay owned by the caller.
 void* orc_decoder_create(const uint8_t* weights, const uint64_t* layers, const uint64_t* top, const int* dims,
                          float epsilon, const float* cosines, const float* sines) {
     auto* m = new DecoderOracle{};
@@ -1647,6 +1764,8 @@ void* orc_decoder_create(const uint8_t* weights, const uint64_t* layers, const u
     m->token_embedding = top[0];
     m->output_norm = top[1];
     m->output = top[2];
+    m->embedding_encoding = static_cast<int>(top[3]);
+    m->output_encoding = static_cast<int>(top[4]);
     m->epsilon = epsilon;
     m->cosines.assign(cosines, cosines + static_cast<size_t>(context) * (m->head_dim / 2));
     m->sines.assign(sines, sines + static_cast<size_t>(context) * (m->head_dim / 2));
@@ -1685,38 +1804,44 @@ int orc_decoder_forward(void* handle, const int32_t* tokens, int count, float* l
     std::vector<float> attention(hidden.size());
     std::vector<float> gate_up(static_cast<size_t>(count) * 2 * ffn);
     std::vector<float> activated(static_cast<size_t>(count) * ffn);
-    // synapse_embed_q8_0 (elementwise.cu:3-15).
-    const size_t row_bytes = static_cast<size_t>(h / 32) * 34;
+    // synapse_embed_q8_0 (elementwise.cu:3-15); K-quant tables as synapse_kq_embed (matmul_kquant.metal:293-308).
+    const size_t row_bytes = row_bytes_of(m.embedding_encoding, h);
     for (int t = 0; t < count; ++t) {
         const uint8_t* row = m.weights + m.token_embedding + static_cast<size_t>(tokens[4 * t + 1]) * row_bytes;
         for (int c = 0; c < h; ++c) {
-            const uint8_t* block = row + static_cast<size_t>(c / 32) * 34;
-            hidden[static_cast<size_t>(t) * h + c] = q8_scale(block) * static_cast<float>(static_cast<int8_t>(block[2 + c % 32]));
+            float& value = hidden[static_cast<size_t>(t) * h + c];
+            if (m.embedding_encoding == 8) {
+                const uint8_t* block = row + static_cast<size_t>(c / 32) * 34;
+                value = q8_scale(block) * static_cast<float>(static_cast<int8_t>(block[2 + c % 32]));
+            } else {
+                value = kq_value(m.embedding_encoding, row, c);
+            }
         }
     }
     for (int layer = 0; layer < m.layer_count; ++layer) {
         const uint64_t* o = &m.layers[static_cast<size_t>(layer) * 15];
+        auto enc = [&](int matrix) { return static_cast<int>((o[14] >> (4 * matrix)) & 0xF); };
         // attention_half (step/layers.rs:62-108).
         for (int t = 0; t < count; ++t) {
             rms_norm_row(&hidden[static_cast<size_t>(t) * h], f32_at(m, o[0]), h, m.epsilon,
                          &normalized[static_cast<size_t>(t) * h]);
         }
-        project_rows(m, o[1], o[4], h, h, count, normalized.data(), h, qkv.data(), qkv_width, 0, false, threads);
-        project_rows(m, o[2], o[5], kv, h, count, normalized.data(), h, qkv.data(), qkv_width, h, false, threads);
-        project_rows(m, o[3], o[6], kv, h, count, normalized.data(), h, qkv.data(), qkv_width, h + kv, false, threads);
+        project_rows(m, o[1], o[4], enc(0), h, h, count, normalized.data(), h, qkv.data(), qkv_width, 0, false, threads);
+        project_rows(m, o[2], o[5], enc(1), kv, h, count, normalized.data(), h, qkv.data(), qkv_width, h, false, threads);
+        project_rows(m, o[3], o[6], enc(2), kv, h, count, normalized.data(), h, qkv.data(), qkv_width, h + kv, false, threads);
         const int appended = orc_paged_append_rope(m.cache, layer, qkv.data(), qkv_width, m.cosines.data(), m.sines.data());
         if (appended != 0) {
             return appended;
         }
         orc_paged_attention(m.cache, layer, qkv.data(), qkv_width, attention.data(), h, threads);
-        project_rows(m, o[9], kNoTensor, h, h, count, attention.data(), h, hidden.data(), h, 0, true, threads);
+        project_rows(m, o[9], kNoTensor, enc(3), h, h, count, attention.data(), h, hidden.data(), h, 0, true, threads);
         // feed_forward_half (step/layers.rs:150-206).
         for (int t = 0; t < count; ++t) {
             rms_norm_row(&hidden[static_cast<size_t>(t) * h], f32_at(m, o[10]), h, m.epsilon,
                          &normalized[static_cast<size_t>(t) * h]);
         }
-        project_rows(m, o[11], kNoTensor, ffn, h, count, normalized.data(), h, gate_up.data(), 2 * ffn, 0, false, threads);
-        project_rows(m, o[12], kNoTensor, ffn, h, count, normalized.data(), h, gate_up.data(), 2 * ffn, ffn, false,
+        project_rows(m, o[11], kNoTensor, enc(4), ffn, h, count, normalized.data(), h, gate_up.data(), 2 * ffn, 0, false, threads);
+        project_rows(m, o[12], kNoTensor, enc(5), ffn, h, count, normalized.data(), h, gate_up.data(), 2 * ffn, ffn, false,
                      threads);
         for (int t = 0; t < count; ++t) {
             for (int c = 0; c < ffn; ++c) {
@@ -1725,7 +1850,7 @@ int orc_decoder_forward(void* handle, const int32_t* tokens, int count, float* l
                     gate / (1.0f + std::exp(-gate)) * gate_up[static_cast<size_t>(t) * 2 * ffn + ffn + c];
             }
         }
-        project_rows(m, o[13], kNoTensor, h, ffn, count, activated.data(), ffn, hidden.data(), h, 0, true, threads);
+        project_rows(m, o[13], kNoTensor, enc(6), h, ffn, count, activated.data(), ffn, hidden.data(), h, 0, true, threads);
     }
     // logits (step/layers.rs:208-228): the gathered rows in token order.
     int rows = 0;
@@ -1737,7 +1862,7 @@ int orc_decoder_forward(void* handle, const int32_t* tokens, int count, float* l
         }
     }
     if (rows > 0) {
-        project_rows(m, m.output, kNoTensor, m.vocabulary, h, rows, normalized.data(), h, logits, m.vocabulary, 0, false,
+        project_rows(m, m.output, kNoTensor, m.output_encoding, m.vocabulary, h, rows, normalized.data(), h, logits, m.vocabulary, 0, false,
                      threads);
     }
     return 0;

@@ -5,7 +5,7 @@
 // residual) -> output norm of the logits rows -> logits projection.
 //
 // The model is composed from this library's own handles: a SynapseKvCache (pages, RoPE, attention) and a
-// SynapseKvWeights (Q8_0 matrices repacked for the MFMA projection kernels), on one stream. The kernels here are the
+// SynapseKvWeights (Q8_0, Q4_K and Q6_K matrices repacked for the MFMA projection kernels), on one stream. The kernels here are the
 // elementwise ones (elementwise.cu / elementwise.metal): embedding lookup, RMS normalization and SwiGLU.
 
 #include <algorithm>
@@ -16,13 +16,12 @@
 #include <vector>
 
 #include "abi_support.h"
+#include "kquant_layout.h"
 #include "kv_internal.h"
 
 namespace synapse_kv {
 namespace {
 
-constexpr uint32_t kEncodingQ4K = 12;
-constexpr uint32_t kEncodingQ6K = 14;
 constexpr uint32_t kMatrices = 7;  // Q, K, V, O, gate, up, down (the packing order of `encodings`)
 
 __device__ inline float half_bits_to_float(uint16_t bits) {
@@ -43,6 +42,30 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* table, uint32
         const uint16_t scale = static_cast<uint16_t>(block[0] | (block[1] << 8));
         const int8_t code = static_cast<int8_t>(block[2 + column % 32]);
         out[column] = half_bits_to_float(scale) * static_cast<float>(code);
+    }
+}
+
+// synapse_kq_embed (matmul_kquant.metal:293-308): hidden[t][c] is value c of the token's K-quant row, decoded as
+// kq_values8 does ((d * sc) * q - dmin * m for Q4_K, (d * scale) * (q - 32) for Q6_K), one workgroup per token.
+template <uint32_t E>
+__global__ __launch_bounds__(256) void embed_kquant_kernel(const uint8_t* table, uint32_t row_bytes,
+                                                           const int32_t* tokens, uint32_t columns, float* hidden) {
+#pragma clang fp contract(off)
+    const int token = blockIdx.x;
+    const uint8_t* row = table + static_cast<uint64_t>(tokens[token]) * row_bytes;
+    float* out = hidden + static_cast<size_t>(token) * columns;
+    for (uint32_t column = threadIdx.x; column < columns; column += blockDim.x) {
+        const uint8_t* block = row + static_cast<size_t>(column / kSuperBlockValues) * ggml_block_bytes(E);
+        const int i = static_cast<int>(column % kSuperBlockValues);
+        const float q = static_cast<float>(kq_code(E, block, i));
+        if constexpr (E == kEncodingQ4K) {
+            int sc = 0;
+            int m = 0;
+            q4k_scale_min(block + 4, i / 32, sc, m);
+            out[column] = (kq_half(block) * static_cast<float>(sc)) * q - kq_half(block + 2) * static_cast<float>(m);
+        } else {
+            out[column] = (kq_half(block + 208) * static_cast<float>(static_cast<int8_t>(block[192 + i / 16]))) * q;
+        }
     }
 }
 
@@ -151,7 +174,7 @@ struct SynapseKvDecoder {
     SynapseKvCache* cache = nullptr;
     SynapseKvWeights* weights = nullptr;
     uint32_t output_matrix = 0;  // index of the logits matrix in `weights`
-    synapse_kv::Buffer<uint8_t> embedding;  // vocabulary rows of GGML Q8_0 blocks
+    synapse_kv::Buffer<uint8_t> embedding;  // vocabulary rows of GGML blocks (Q8_0, Q4_K or Q6_K)
     synapse_kv::Buffer<float> norms;        // per layer [attention norm | feed-forward norm], then the output norm
     synapse_kv::Buffer<float> hidden;       // [step_tokens][hidden]: the residual stream
     synapse_kv::Buffer<float> normalized;   // [step_tokens][hidden]
@@ -186,14 +209,10 @@ struct SynapseKvDecoder {
 namespace synapse_kv {
 namespace {
 
-// Encoding::from_id (decoder/encoding.rs:26-36) with this build's kernels: Q8_0 only.
+// Encoding::from_id (decoder/encoding.rs:26-36).
 void check_encoding(uint32_t id, const std::string& name) {
-    if (id == SYNAPSE_KV_ENCODING_Q8_0) {
+    if (id == SYNAPSE_KV_ENCODING_Q8_0 || is_kquant(id)) {
         return;
-    }
-    if (id == kEncodingQ4K || id == kEncodingQ6K) {
-        fail(SYNAPSE_KV_UNAVAILABLE, name + ": K-quant matrices (GGML type " + std::to_string(id) +
-                                         ") are not implemented by these kernels; Q8_0 is");
     }
     fail(SYNAPSE_KV_UNAVAILABLE, name + ": the GPU kernels implement Q8_0, Q4_K, and Q6_K matrices, not GGML type " +
                                      std::to_string(id));
@@ -210,11 +229,12 @@ void check_span(const SynapseKvDecoderDesc& d, uint64_t offset, uint64_t bytes, 
 void check_matrix(const SynapseKvDecoderDesc& d, uint64_t offset, uint64_t rows, uint64_t columns, uint32_t encoding,
                   const std::string& name) {
     check_encoding(encoding, name);
-    if (columns % 32 != 0) {
+    const uint64_t values = static_cast<uint64_t>(ggml_block_values(encoding));
+    if (columns % values != 0) {
         fail(SYNAPSE_KV_UNAVAILABLE, "tensor " + name + " has " + std::to_string(columns) +
-                                         " columns, not a multiple of its 32-value blocks");
+                                         " columns, not a multiple of its " + std::to_string(values) + "-value blocks");
     }
-    check_span(d, offset, rows * (columns / 32) * 34, 2, name);
+    check_span(d, offset, ggml_matrix_bytes(encoding, rows, columns), 2, name);
 }
 
 void check_f32(const SynapseKvDecoderDesc& d, uint64_t offset, uint64_t values, const std::string& name) {
@@ -321,8 +341,12 @@ void create_decoder(const SynapseKvDecoderDesc& d, int32_t device, SynapseKvDeco
 
     // Matrices: per layer Q, K, V (with their biases), O, gate, up, down; then the logits matrix.
     std::vector<SynapseKvMatrix> matrices;
+    std::vector<uint32_t> encodings;
     for (uint32_t index = 0; index < d.layer_count; ++index) {
         const SynapseKvLayerOffsets& l = d.layers[index];
+        for (uint32_t matrix = 0; matrix < kMatrices; ++matrix) {
+            encodings.push_back(encoding_of(l, matrix));
+        }
         matrices.push_back({l.query, l.query_bias, d.hidden, d.hidden});
         matrices.push_back({l.key, l.key_bias, static_cast<uint32_t>(kv), d.hidden});
         matrices.push_back({l.value, l.value_bias, static_cast<uint32_t>(kv), d.hidden});
@@ -332,13 +356,14 @@ void create_decoder(const SynapseKvDecoderDesc& d, int32_t device, SynapseKvDeco
         matrices.push_back({l.down, SYNAPSE_KV_NO_BIAS, d.hidden, d.feed_forward});
     }
     matrices.push_back({d.output, SYNAPSE_KV_NO_BIAS, d.vocabulary, d.hidden});
+    encodings.push_back(d.output_encoding);
     model->output_matrix = static_cast<uint32_t>(matrices.size() - 1);
     check_hip(hipSetDevice(device), "set device");
-    check_status(synapse_kv_weights_create(d.weights, d.weights_length, matrices.data(),
-                                           static_cast<uint32_t>(matrices.size()), &model->weights));
+    check_status(synapse_kv_weights_create_encoded(d.weights, d.weights_length, matrices.data(), encodings.data(),
+                                                   static_cast<uint32_t>(matrices.size()), &model->weights));
 
     // Embedding table (GGML rows, looked up per token), norms.
-    const size_t embedding_bytes = static_cast<size_t>(d.vocabulary) * (d.hidden / 32) * 34;
+    const size_t embedding_bytes = ggml_matrix_bytes(d.embedding_encoding, d.vocabulary, d.hidden);
     model->embedding.allocate(embedding_bytes, "token embedding");
     check_hip(hipMemcpy(model->embedding.pointer, d.weights + d.token_embedding, embedding_bytes, hipMemcpyHostToDevice),
               "token embedding upload");
@@ -466,9 +491,21 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
     const uint32_t kv = d.kv_heads * d.head_dim;
     const uint32_t qkv_width = hidden + 2 * kv;
     const uint32_t ffn = d.feed_forward;
-    const uint32_t row_bytes = (hidden / 32) * 34;
-    hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, m.stream, m.embedding.pointer, row_bytes,
-                       m.indices.pointer, hidden, m.hidden.pointer);
+    const uint32_t row_bytes = static_cast<uint32_t>(ggml_matrix_bytes(d.embedding_encoding, 1, hidden));
+    switch (d.embedding_encoding) {
+        case kEncodingQ4K:
+            hipLaunchKernelGGL(embed_kquant_kernel<kEncodingQ4K>, dim3(n), dim3(256), 0, m.stream, m.embedding.pointer,
+                               row_bytes, m.indices.pointer, hidden, m.hidden.pointer);
+            break;
+        case kEncodingQ6K:
+            hipLaunchKernelGGL(embed_kquant_kernel<kEncodingQ6K>, dim3(n), dim3(256), 0, m.stream, m.embedding.pointer,
+                               row_bytes, m.indices.pointer, hidden, m.hidden.pointer);
+            break;
+        default:
+            hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, m.stream, m.embedding.pointer, row_bytes,
+                               m.indices.pointer, hidden, m.hidden.pointer);
+            break;
+    }
     check_hip(hipGetLastError(), "embedding");
     for (uint32_t layer = 0; layer < d.layer_count; ++layer) {
         const uint32_t base = layer * kMatrices;

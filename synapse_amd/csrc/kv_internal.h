@@ -166,7 +166,7 @@ struct GatherArgs {
 // first_tile .. first_tile + q8_tiles(rows) - 1 of the launch.
 struct ProjectionSegment {
     const uint8_t* codes;
-    const uint16_t* scales;  // FP16 bits
+    const void* scales;  // Q8_0: FP16 bits; K-quants: FP32 factors (kquant_layout.h)
     const float* bias;       // null: no bias
     int32_t rows;
     int32_t first_tile;
@@ -191,6 +191,9 @@ struct ProjectionArgs {
     int32_t slices;          // decode: column slices (projection_decode_slices)
     float* partials;         // decode: [slices][16][partial_stride] per-slice sums (scratch)
     int64_t partial_stride;  // total_tiles * 16
+    uint32_t encoding;       // GGML type of every segment: 8 (Q8_0), 12 (Q4_K) or 14 (Q6_K)
+    int32_t pad;
+    float* sums;             // prompt runs of Q4_K: [tokens][padded_columns / 8] sums of 8 inputs (scratch)
 };
 
 // KV page activation (ADR-016). Key summaries live in their own buffer, one summary page per pool page:

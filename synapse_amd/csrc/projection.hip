@@ -17,6 +17,11 @@
 // slice of at most eight 64-column chunks; the workgroup splits its input slice into LDS once and every wave streams
 // its tile's codes and scales against it (see below); reduce_kernel adds the slices in order with bias and residual.
 //
+// K-quant matrices (Q4_K, Q6_K; kquant_layout.h) run the same kernels specialised on the encoding: a block's codes
+// are exact in bf16 too (0..15, -32..31), and its FP32 factors are applied to the block's exact-product sum. Q4_K
+// subtracts offset * sum(x) with the block's input sums (LDS in the decode kernel, written by split_kernel for prompt
+// runs); Q6_K multiplies each 16-column half on its own (the other half's A fragments zeroed) and scales each.
+//
 // Prompt runs: split_kernel writes the three parts of the whole input once, in the B-operand fragment order of the
 // MFMA, and project_kernel<4> runs one workgroup per (16-row tile, 64 tokens); its four waves split the columns
 // into contiguous ranges of 64-column chunks and load, per chunk, the tile's 1 KiB of codes (one 16-byte load per
@@ -25,6 +30,7 @@
 // in wave order, then the bias and the residual.
 
 #include "kv_internal.h"
+#include "kquant_layout.h"
 #include "q8_layout.h"
 
 namespace synapse_kv {
@@ -106,6 +112,14 @@ __global__ __launch_bounds__(256) void split_kernel(ProjectionArgs a) {
     for (int p = 0; p < kParts; ++p) {
         *reinterpret_cast<bf16x8*>(a.parts + part_offset(a.chunks, token, column, p)) = parts[p];
     }
+    if (a.sums != nullptr) {
+        float sum = values[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) {
+            sum += values[i];
+        }
+        a.sums[static_cast<size_t>(token) * groups + column / 8] = sum;
+    }
 }
 
 // Per token tile and block, the three parts of columns 8 g .. 8 g + 7 of token 16 c + r (B fragments).
@@ -122,53 +136,182 @@ constexpr int projection_batch() {
     return 2;
 }
 
-// One chunk (two blocks): each block's three part products go to their own fresh accumulator, issued part by part
-// across blocks and token tiles so a dependent MFMA is 2 NT MFMAs behind the one it needs, and the block sums are
-// scaled into the running sums after all of them were issued.
-template <int NT>
-__device__ inline void multiply_chunk(uintx4 codes, uintx4 scales, const InputFragments<NT>& input, floatx4 (&acc)[NT]) {
-    bf16x8 weight[2];
-    float d[2][4];
+// One chunk of one 16-row tile as a lane loads it: its codes (16 bytes of int8 codes; Q4_K: 8 bytes of nibbles in
+// .xy) and the factors of its accumulator rows (Q8_0: eight FP16 scales; K-quants: sixteen FP32 factors, [field]
+// [block][row]).
+template <uint32_t E>
+struct ChunkWeights {
+    uintx4 codes;
+    uintx4 scales[E == kEncodingQ8_0 ? 1 : 4];
+};
+
+// Loads chunk `tile_chunk` (tile * chunks + chunk) of a matrix for lane `lane` of row group g.
+template <uint32_t E>
+__device__ inline ChunkWeights<E> load_chunk(const uint8_t* codes, const void* scales, size_t tile_chunk, int lane,
+                                             int g) {
+    ChunkWeights<E> w;
+    if constexpr (E == kEncodingQ4K) {
+        const uintx2 half = __builtin_nontemporal_load(reinterpret_cast<const uintx2*>(codes + tile_chunk * kQ4KTileBytes) + lane);
+        w.codes = uintx4{half.x, half.y, 0u, 0u};
+    } else {
+        w.codes = __builtin_nontemporal_load(reinterpret_cast<const uintx4*>(codes + tile_chunk * kQ8TileBytes) + lane);
+    }
+    if constexpr (E == kEncodingQ8_0) {
+        w.scales[0] = reinterpret_cast<const uintx4*>(static_cast<const uint16_t*>(scales) + tile_chunk * kQ8TileScales)[g];
+    } else {
+        const uintx4* factors = reinterpret_cast<const uintx4*>(static_cast<const float*>(scales) + tile_chunk * kKTileScales) + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w.scales[i] = factors[i];
+        }
+    }
+    return w;
+}
+
+// FP32 factor i of a lane's factor vector. The element is copied out first: a vector element is not an object of
+// its own, and a bit cast of the element expression would read the vector's first element.
+__device__ inline float factor(uintx4 v, int i) {
+    const uint32_t bits = v[i];
+    return __builtin_bit_cast(float, bits);
+}
+
+// The chunk's two blocks of A fragments: eight codes of one row per block, exact in bf16.
+template <uint32_t E>
+__device__ inline void weight_fragments(uintx4 codes, bf16x8 (&weight)[2]) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
-            const uint32_t word = codes[2 * b + w];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                weight[b][4 * w + i] = static_cast<__bf16>(static_cast<float>(static_cast<int8_t>((word >> (8 * i)) & 0xFF)));
-            }
-            const uint32_t pair = scales[2 * b + w];
-            d[b][2 * w] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair & 0xFFFF)));
-            d[b][2 * w + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> 16)));
-        }
-    }
-    floatx4 block[2][NT];
-#pragma unroll
-    for (int p = kParts - 1; p >= 0; --p) {
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-#pragma unroll
-            for (int c = 0; c < NT; ++c) {
-                block[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    weight[b], input.x[c][b][p], p == kParts - 1 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : block[b][c], 0,
-                    0, 0);
-            }
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-        for (int c = 0; c < NT; ++c) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[c][i] = __builtin_fmaf(block[b][c][i], d[b][i], acc[c][i]);
+                int code;
+                if constexpr (E == kEncodingQ4K) {
+                    code = static_cast<int>((codes[w] >> (8 * i + 4 * b)) & 0xF);
+                } else {
+                    code = static_cast<int8_t>((codes[2 * b + w] >> (8 * i)) & 0xFF);
+                }
+                weight[b][4 * w + i] = static_cast<__bf16>(static_cast<float>(code));
             }
         }
     }
 }
 
-template <int NT>
+// One chunk (two blocks): each block's three part products go to their own fresh accumulator, issued part by part
+// across blocks and token tiles so a dependent MFMA is 2 NT MFMAs behind the one it needs, and the block sums are
+// scaled into the running sums after all of them were issued.
+//   Q8_0: acc += d * (codes . x) per block (matmul.cu:101-104).
+//   Q4_K: acc += scale * (codes . x) - offset * sum(x) per block, with sum(x) the block's input sum per token in
+//         `xsum` (kq_apply, matmul_kquant.metal:115-119).
+//   Q6_K: the block's two 16-column halves have their own scales: the A fragments of lane groups 0-1 (columns
+//         0-15) and 2-3 (columns 16-31) are multiplied separately (the other half zeroed) and each sum scaled.
+template <uint32_t E, int NT>
+__device__ inline void multiply_chunk(const ChunkWeights<E>& w, const InputFragments<NT>& input,
+                                      const float (&xsum)[NT][2], floatx4 (&acc)[NT]) {
+    bf16x8 weight[2];
+    weight_fragments<E>(w.codes, weight);
+    if constexpr (E == kEncodingQ8_0) {
+        float d[2][4];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t pair = w.scales[0][2 * b + h];
+                d[b][2 * h] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair & 0xFFFF)));
+                d[b][2 * h + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> 16)));
+            }
+        }
+        floatx4 block[2][NT];
+#pragma unroll
+        for (int p = kParts - 1; p >= 0; --p) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                for (int c = 0; c < NT; ++c) {
+                    block[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        weight[b], input.x[c][b][p], p == kParts - 1 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : block[b][c],
+                        0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[c][i] = __builtin_fmaf(block[b][c][i], d[b][i], acc[c][i]);
+                }
+            }
+        }
+    } else if constexpr (E == kEncodingQ4K) {
+        floatx4 block[2][NT];
+#pragma unroll
+        for (int p = kParts - 1; p >= 0; --p) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                for (int c = 0; c < NT; ++c) {
+                    block[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        weight[b], input.x[c][b][p], p == kParts - 1 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : block[b][c],
+                        0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float scale = factor(w.scales[b], i);
+                    const float offset = factor(w.scales[2 + b], i);
+                    acc[c][i] = __builtin_fmaf(block[b][c][i], scale, acc[c][i]);
+                    acc[c][i] = __builtin_fmaf(-offset, xsum[c][b], acc[c][i]);
+                }
+            }
+        }
+    } else {
+        const bool first_half = (threadIdx.x & 63) < 32;  // lane groups 0 and 1
+        const bf16x8 zero = bf16x8{};
+        bf16x8 halves[2][2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            halves[0][b] = first_half ? weight[b] : zero;
+            halves[1][b] = first_half ? zero : weight[b];
+        }
+        floatx4 block[2][2][NT];
+#pragma unroll
+        for (int p = kParts - 1; p >= 0; --p) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                    for (int c = 0; c < NT; ++c) {
+                        block[h][b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            halves[h][b], input.x[c][b][p],
+                            p == kParts - 1 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : block[h][b][c], 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                for (int c = 0; c < NT; ++c) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc[c][i] = __builtin_fmaf(block[h][b][c][i], factor(w.scales[2 * h + b], i), acc[c][i]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <uint32_t E, int NT>
 __global__ __launch_bounds__(projection_waves<NT>() * 64) void project_kernel(ProjectionArgs a) {
     constexpr int kWaves = projection_waves<NT>();
     constexpr int kBatch = projection_batch<NT>();
@@ -187,17 +330,17 @@ __global__ __launch_bounds__(projection_waves<NT>() * 64) void project_kernel(Pr
     const int chunks = a.chunks;
     const int begin = wave * chunks / kWaves;
     const int end = (wave + 1) * chunks / kWaves;
+    const size_t tile_chunks = static_cast<size_t>(tile) * chunks;
 
-    const uintx4* codes = reinterpret_cast<const uintx4*>(seg.codes + static_cast<size_t>(tile) * chunks * kQ8TileBytes) + lane;
-    // A chunk's 32 scales are 64 bytes: four 16-byte groups, one per row group g.
-    const uintx4* scales = reinterpret_cast<const uintx4*>(seg.scales + static_cast<size_t>(tile) * chunks * kQ8TileScales) + g;
     // The split input's token tiles of this workgroup (a tile past the last token re-reads tile 0; never written).
     const bf16x8* tiles[NT];
+    const float* sums[NT];
 #pragma unroll
     for (int c = 0; c < NT; ++c) {
         const int tile_index = blockIdx.y * NT + c;
-        tiles[c] = reinterpret_cast<const bf16x8*>(a.parts) +
-                   static_cast<size_t>(16 * tile_index < a.tokens ? tile_index : 0) * chunks * (kParts * 2 * 64) + lane;
+        const int source = 16 * tile_index < a.tokens ? tile_index : 0;
+        tiles[c] = reinterpret_cast<const bf16x8*>(a.parts) + static_cast<size_t>(source) * chunks * (kParts * 2 * 64) + lane;
+        sums[c] = a.sums + static_cast<size_t>(16 * source + (lane & 15)) * (a.padded_columns / 8);
     }
 
     floatx4 acc[NT];
@@ -210,8 +353,8 @@ __global__ __launch_bounds__(projection_waves<NT>() * 64) void project_kernel(Pr
     // of the multiplies.
     for (int first = begin; first < end; first += kBatch) {
         InputFragments<NT> input[kBatch];
-        uintx4 batch_codes[kBatch];
-        uintx4 batch_scales[kBatch];
+        ChunkWeights<E> weights[kBatch];
+        floatx4 raw_sums[kBatch][NT][2];
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
             const int chunk = min(first + i, end - 1);
@@ -226,14 +369,33 @@ __global__ __launch_bounds__(projection_waves<NT>() * 64) void project_kernel(Pr
                     }
                 }
             }
-            batch_codes[i] = __builtin_nontemporal_load(codes + static_cast<size_t>(chunk) * 64);
-            batch_scales[i] = scales[static_cast<size_t>(chunk) * 4];
+            weights[i] = load_chunk<E>(seg.codes, seg.scales, tile_chunks + chunk, lane, g);
+            if constexpr (E == kEncodingQ4K) {
+#pragma unroll
+                for (int c = 0; c < NT; ++c) {
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        raw_sums[i][c][b] = reinterpret_cast<const floatx4*>(sums[c] + chunk * 8 + 4 * b)[0];
+                    }
+                }
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < kBatch; ++i) {
             if (first + i < end) {
-                multiply_chunk<NT>(batch_codes[i], batch_scales[i], input[i], acc);
+                float xsum[NT][2] = {};
+                if constexpr (E == kEncodingQ4K) {
+#pragma unroll
+                    for (int c = 0; c < NT; ++c) {
+#pragma unroll
+                        for (int b = 0; b < 2; ++b) {
+                            const floatx4 four = raw_sums[i][c][b];
+                            xsum[c][b] = ((four[0] + four[1]) + four[2]) + four[3];
+                        }
+                    }
+                }
+                multiply_chunk<E, NT>(weights[i], input[i], xsum, acc);
             }
         }
     }
@@ -293,9 +455,12 @@ __device__ inline int locate_tile(const ProjectionArgs& a, int tile, ProjectionS
     return tile - seg.first_tile;
 }
 
+template <uint32_t E>
 __global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(ProjectionArgs a) {
     constexpr int kItems = kDecodeSliceChunks * 128 / (kDecodeTiles * 64);  // split items per thread
     __shared__ bf16x8 staged[kDecodeSliceChunks * kParts * 2 * 64];
+    // Q4_K: per chunk, 8-column group and token, the sum of the 8 inputs.
+    __shared__ float group_sums[E == kEncodingQ4K ? kDecodeSliceChunks * 8 * 16 : 1];
     const int slice = blockIdx.y;
     const int k0 = slice * a.chunks / a.slices;
     const int k1 = (slice + 1) * a.chunks / a.slices;
@@ -328,17 +493,11 @@ __global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(Proje
     //    so the split below waits for the input only, while the weight stream stays in flight.
     ProjectionSegment seg;
     const int tile = locate_tile(a, global_tile, seg);
-    const uintx4* codes =
-        reinterpret_cast<const uintx4*>(seg.codes + (static_cast<size_t>(tile) * a.chunks + k0) * kQ8TileBytes) + lane;
-    const uintx4* scales =
-        reinterpret_cast<const uintx4*>(seg.scales + (static_cast<size_t>(tile) * a.chunks + k0) * kQ8TileScales) + g;
-    uintx4 batch_codes[kDecodeSliceChunks];
-    uintx4 batch_scales[kDecodeSliceChunks];
+    const size_t first_chunk = static_cast<size_t>(tile) * a.chunks + k0;
+    ChunkWeights<E> batch[kDecodeSliceChunks];
 #pragma unroll
     for (int i = 0; i < kDecodeSliceChunks; ++i) {
-        const int chunk = min(i, count - 1);
-        batch_codes[i] = __builtin_nontemporal_load(codes + static_cast<size_t>(chunk) * 64);
-        batch_scales[i] = scales[static_cast<size_t>(chunk) * 4];
+        batch[i] = load_chunk<E>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
     }
     __builtin_amdgcn_sched_barrier(0);
     // 3. Split into the three bf16 parts, in B-fragment order, into LDS.
@@ -366,6 +525,14 @@ __global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(Proje
         for (int p = 0; p < kParts; ++p) {
             staged[((chunk * kParts + p) * 2 + block) * 64 + 16 * lane_group + t] = parts[p];
         }
+        if constexpr (E == kEncodingQ4K) {
+            float sum = raw[j][0][0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) {
+                sum += raw[j][i / 4][i % 4];
+            }
+            group_sums[(chunk * 8 + (group & 7)) * 16 + t] = sum;
+        }
     }
     __syncthreads();
 
@@ -382,7 +549,15 @@ __global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(Proje
                     input.x[0][b][p] = staged[((i * kParts + p) * 2 + b) * 64 + lane];
                 }
             }
-            multiply_chunk<1>(batch_codes[i], batch_scales[i], input, acc);
+            float xsum[1][2] = {};
+            if constexpr (E == kEncodingQ4K) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const float* four = group_sums + (i * 8 + 4 * b) * 16 + (lane & 15);
+                    xsum[0][b] = ((four[0] + four[16]) + four[32]) + four[48];
+                }
+            }
+            multiply_chunk<E, 1>(batch[i], input, xsum, acc);
         }
     }
     if (blockIdx.x * kDecodeTiles + wave >= a.total_tiles) {
@@ -442,20 +617,40 @@ int projection_token_tiles(int tokens) { return tokens <= 16 ? 1 : 4; }
 int projection_decode_slices(int chunks) { return (chunks + kDecodeSliceChunks - 1) / kDecodeSliceChunks; }
 
 hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles) {
+    const Launch plain{launch.stream, nullptr, nullptr};
     if (args.tokens <= 16) {
         const dim3 grid((tiles + kDecodeTiles - 1) / kDecodeTiles, args.slices);
-        SYNAPSE_KV_LAUNCH(project_decode_kernel, grid, dim3(kDecodeTiles * 64), launch, args);
+        switch (args.encoding) {
+            case kEncodingQ4K:
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ4K>, grid, dim3(kDecodeTiles * 64), launch, args);
+                break;
+            case kEncodingQ6K:
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ6K>, grid, dim3(kDecodeTiles * 64), launch, args);
+                break;
+            default:
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ8_0>, grid, dim3(kDecodeTiles * 64), launch, args);
+                break;
+        }
         const int outputs = args.tokens * tiles * kQ8TileRows;
-        SYNAPSE_KV_LAUNCH(reduce_kernel, dim3((outputs + 255) / 256), dim3(256), (Launch{launch.stream, nullptr, nullptr}),
-                          args);
+        SYNAPSE_KV_LAUNCH(reduce_kernel, dim3((outputs + 255) / 256), dim3(256), plain, args);
         return hipGetLastError();
     }
     const int splits = args.tokens * (args.padded_columns / 8);
-    SYNAPSE_KV_LAUNCH(split_kernel, dim3((splits + 255) / 256), dim3(256), (Launch{launch.stream, nullptr, nullptr}),
-                      args);
+    SYNAPSE_KV_LAUNCH(split_kernel, dim3((splits + 255) / 256), dim3(256), plain, args);
     const int per_block = 16 * projection_token_tiles(args.tokens);
     const dim3 grid(tiles, (args.tokens + per_block - 1) / per_block);
-    SYNAPSE_KV_LAUNCH(project_kernel<4>, grid, dim3(projection_waves<4>() * 64), launch, args);
+    const dim3 block(projection_waves<4>() * 64);
+    switch (args.encoding) {
+        case kEncodingQ4K:
+            SYNAPSE_KV_LAUNCH((project_kernel<kEncodingQ4K, 4>), grid, block, launch, args);
+            break;
+        case kEncodingQ6K:
+            SYNAPSE_KV_LAUNCH((project_kernel<kEncodingQ6K, 4>), grid, block, launch, args);
+            break;
+        default:
+            SYNAPSE_KV_LAUNCH((project_kernel<kEncodingQ8_0, 4>), grid, block, launch, args);
+            break;
+    }
     return hipGetLastError();
 }
 

@@ -12,6 +12,7 @@
 
 #include "abi_support.h"
 #include "kv_internal.h"
+#include "kquant_layout.h"
 #include "q8_layout.h"
 
 namespace synapse_kv {
@@ -24,6 +25,7 @@ struct DeviceMatrix {
     size_t scales = 0;
     size_t bias = 0;
     bool has_bias = false;
+    uint32_t encoding = kEncodingQ8_0;  // GGML type id
 };
 
 size_t align_to(size_t value, size_t alignment) { return (value + alignment - 1) / alignment * alignment; }
@@ -75,8 +77,8 @@ void check_device_pointer(SynapseKvWeights& weights, const void* pointer, const 
     }
 }
 
-void create_weights(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMatrix* matrices, uint32_t count,
-                    SynapseKvWeights** out) {
+void create_weights(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMatrix* matrices, const uint32_t* encodings,
+                    uint32_t count, SynapseKvWeights** out) {
     if (count == 0) {
         invalid("at least one matrix");
     }
@@ -84,13 +86,19 @@ void create_weights(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMat
     size_t total = 0;
     for (uint32_t index = 0; index < count; ++index) {
         const SynapseKvMatrix& m = matrices[index];
+        const uint32_t encoding = encodings != nullptr ? encodings[index] : kEncodingQ8_0;
         const std::string name = "matrix " + std::to_string(index);
-        if (m.rows == 0 || m.columns == 0 || m.columns % kQ8BlockElements != 0) {
-            invalid(name + ": rows must be positive and columns a positive multiple of 32");
+        if (encoding != kEncodingQ8_0 && !is_kquant(encoding)) {
+            fail(SYNAPSE_KV_UNAVAILABLE, name + ": the kernels implement Q8_0, Q4_K, and Q6_K matrices, not GGML type " +
+                                             std::to_string(encoding));
         }
-        const uint64_t weight_bytes = static_cast<uint64_t>(m.rows) * (m.columns / kQ8BlockElements) * kQ8BlockBytes;
+        const uint32_t block_values = static_cast<uint32_t>(ggml_block_values(encoding));
+        if (m.rows == 0 || m.columns == 0 || m.columns % block_values != 0) {
+            invalid(name + ": rows must be positive and columns a positive multiple of " + std::to_string(block_values));
+        }
+        const uint64_t weight_bytes = ggml_matrix_bytes(encoding, m.rows, m.columns);
         if (m.weight > blob_bytes || weight_bytes > blob_bytes - m.weight) {
-            invalid(name + ": its Q8_0 rows extend past the blob");
+            invalid(name + ": its rows extend past the blob");
         }
         if (m.bias != SYNAPSE_KV_NO_BIAS &&
             (m.bias > blob_bytes || static_cast<uint64_t>(m.rows) * 4 > blob_bytes - m.bias || m.bias % 4 != 0)) {
@@ -100,10 +108,11 @@ void create_weights(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMat
         d.rows = m.rows;
         d.columns = m.columns;
         const size_t tiles = static_cast<size_t>(q8_tiles(static_cast<int>(m.rows))) * q8_chunks(static_cast<int>(m.columns));
+        d.encoding = encoding;
         d.codes = total;
-        total = align_to(total + tiles * kQ8TileBytes, 256);
+        total = align_to(total + tiles * tile_code_bytes(encoding), 256);
         d.scales = total;
-        total = align_to(total + tiles * kQ8TileScales * sizeof(uint16_t), 256);
+        total = align_to(total + tiles * tile_scale_bytes(encoding), 256);
         d.has_bias = m.bias != SYNAPSE_KV_NO_BIAS;
         if (d.has_bias) {
             d.bias = total;
@@ -114,8 +123,13 @@ void create_weights(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMat
     for (uint32_t index = 0; index < count; ++index) {
         const SynapseKvMatrix& m = matrices[index];
         const DeviceMatrix& d = layout[index];
-        q8_repack(blob + m.weight, static_cast<int>(m.rows), static_cast<int>(m.columns), staging.data() + d.codes,
-                  reinterpret_cast<uint16_t*>(staging.data() + d.scales));
+        if (is_kquant(d.encoding)) {
+            kq_repack(d.encoding, blob + m.weight, static_cast<int>(m.rows), static_cast<int>(m.columns),
+                      staging.data() + d.codes, reinterpret_cast<float*>(staging.data() + d.scales));
+        } else {
+            q8_repack(blob + m.weight, static_cast<int>(m.rows), static_cast<int>(m.columns), staging.data() + d.codes,
+                      reinterpret_cast<uint16_t*>(staging.data() + d.scales));
+        }
         if (d.has_bias) {
             std::memcpy(staging.data() + d.bias, blob + m.bias, static_cast<size_t>(m.rows) * 4);
         }
@@ -134,6 +148,66 @@ void create_weights(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMat
     *out = weights;
 }
 
+// One launch over segments [first, first + count) of the projection, which share an encoding.
+void launch_run(SynapseKvWeights& weights, const SynapseKvProjection& p, uint32_t first, uint32_t count,
+                const float* input, float* output) {
+    ProjectionArgs args{};
+    int tiles = 0;
+    uint32_t columns = 0;
+    for (uint32_t s = 0; s < count; ++s) {
+        const DeviceMatrix& m = weights.matrices[p.matrix[first + s]];
+        columns = m.columns;
+        ProjectionSegment& seg = args.segment[s];
+        seg.codes = weights.memory + m.codes;
+        seg.scales = weights.memory + m.scales;
+        seg.bias = m.has_bias ? reinterpret_cast<const float*>(weights.memory + m.bias) : nullptr;
+        seg.rows = static_cast<int32_t>(m.rows);
+        seg.first_tile = tiles;
+        seg.out_column = static_cast<int32_t>(p.out_column[first + s]);
+        tiles += q8_tiles(static_cast<int>(m.rows));
+    }
+    const uint32_t encoding = weights.matrices[p.matrix[first]].encoding;
+    args.encoding = encoding;
+    args.segments = static_cast<int32_t>(count);
+    args.columns = static_cast<int32_t>(columns);
+    args.chunks = q8_chunks(static_cast<int>(columns));
+    args.tokens = static_cast<int32_t>(p.tokens);
+    args.in_stride = static_cast<int32_t>(p.in_stride);
+    args.out_stride = static_cast<int32_t>(p.out_stride);
+    args.accumulate = static_cast<int32_t>(p.accumulate);
+    args.input = input;
+    args.output = output;
+    args.padded_columns = args.chunks * kQ8ChunkColumns;
+    args.total_tiles = tiles;
+    args.slices = projection_decode_slices(args.chunks);
+    args.partial_stride = static_cast<int64_t>(tiles) * kQ8TileRows;
+    // Scratch: decode keeps per-slice sums ([slices][16][rows]); prompt runs the input's bf16 split in whole 16-token
+    // tiles (the kernel reads every column of a tile; a token past the last only feeds an output that is never
+    // written), followed for Q4_K by the sums of 8 inputs of those tiles.
+    const size_t padded_tokens = static_cast<size_t>((p.tokens + 15) / 16) * 16;
+    const size_t parts_bytes = padded_tokens * args.padded_columns * 3 * sizeof(__bf16);
+    const size_t needed =
+        p.tokens <= 16 ? static_cast<size_t>(args.slices) * 16 * args.partial_stride * sizeof(float)
+                       : parts_bytes + (encoding == kEncodingQ4K ? padded_tokens * (args.padded_columns / 8) * sizeof(float) : 0);
+    if (needed > weights.parts_bytes) {
+        // Work already queued may still read the old scratch.
+        check_hip(hipStreamSynchronize(weights.stream), "drain before reallocation");
+        if (weights.parts != nullptr) {
+            check_hip(hipFree(weights.parts), "projection scratch");
+            weights.parts = nullptr;
+            weights.parts_bytes = 0;
+        }
+        check_hip(hipMalloc(reinterpret_cast<void**>(&weights.parts), needed), "projection scratch");
+        weights.parts_bytes = needed;
+    }
+    args.parts = weights.parts;
+    args.partials = reinterpret_cast<float*>(weights.parts);
+    args.sums = p.tokens > 16 && encoding == kEncodingQ4K
+                    ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(weights.parts) + parts_bytes)
+                    : nullptr;
+    check_hip(launch_projection(Launch{weights.stream, nullptr, nullptr}, args, tiles), "projection");
+}
+
 void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output) {
     if (p.segments < 1 || p.segments > 3) {
         invalid("a projection has 1..3 segments");
@@ -141,8 +215,6 @@ void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const floa
     if (p.tokens == 0 || p.accumulate > 1 || p.reserved != 0) {
         invalid("tokens must be positive, accumulate 0 or 1 and reserved 0");
     }
-    ProjectionArgs args{};
-    int tiles = 0;
     uint32_t columns = 0;
     for (uint32_t s = 0; s < p.segments; ++s) {
         if (p.matrix[s] >= weights.matrices.size()) {
@@ -158,14 +230,6 @@ void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const floa
         if (static_cast<uint64_t>(p.out_column[s]) + m.rows > p.out_stride) {
             invalid("segment " + std::to_string(s) + " writes past out_stride");
         }
-        ProjectionSegment& seg = args.segment[s];
-        seg.codes = weights.memory + m.codes;
-        seg.scales = reinterpret_cast<const uint16_t*>(weights.memory + m.scales);
-        seg.bias = m.has_bias ? reinterpret_cast<const float*>(weights.memory + m.bias) : nullptr;
-        seg.rows = static_cast<int32_t>(m.rows);
-        seg.first_tile = tiles;
-        seg.out_column = static_cast<int32_t>(p.out_column[s]);
-        tiles += q8_tiles(static_cast<int>(m.rows));
     }
     if (p.in_stride < columns || p.in_stride % 4 != 0) {
         invalid("in_stride must be a multiple of 4 and hold the " + std::to_string(columns) + " input columns");
@@ -176,40 +240,17 @@ void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const floa
     check_hip(hipSetDevice(weights.device), "set device");
     check_device_pointer(weights, input, "input");
     check_device_pointer(weights, output, "output");
-    args.segments = static_cast<int32_t>(p.segments);
-    args.columns = static_cast<int32_t>(columns);
-    args.chunks = q8_chunks(static_cast<int>(columns));
-    args.tokens = static_cast<int32_t>(p.tokens);
-    args.in_stride = static_cast<int32_t>(p.in_stride);
-    args.out_stride = static_cast<int32_t>(p.out_stride);
-    args.accumulate = static_cast<int32_t>(p.accumulate);
-    args.input = input;
-    args.output = output;
-    args.padded_columns = args.chunks * kQ8ChunkColumns;
-    args.total_tiles = tiles;
-    args.slices = projection_decode_slices(args.chunks);
-    args.partial_stride = static_cast<int64_t>(tiles) * kQ8TileRows;
-    // Scratch: decode keeps per-slice sums ([slices][16][rows]); prompt runs the input's bf16 split in whole 16-token
-    // tiles (the kernel reads every column of a tile; a token past the last only feeds an output that is never
-    // written).
-    const size_t needed =
-        p.tokens <= 16
-            ? static_cast<size_t>(args.slices) * 16 * args.partial_stride * sizeof(float)
-            : static_cast<size_t>((p.tokens + 15) / 16) * 16 * args.padded_columns * 3 * sizeof(__bf16);
-    if (needed > weights.parts_bytes) {
-        // Work already queued may still read the old scratch.
-        check_hip(hipStreamSynchronize(weights.stream), "drain before reallocation");
-        if (weights.parts != nullptr) {
-            check_hip(hipFree(weights.parts), "projection scratch");
-            weights.parts = nullptr;
-            weights.parts_bytes = 0;
+    // Consecutive segments of one encoding share a launch (the kernels are specialised per encoding).
+    uint32_t first = 0;
+    while (first < p.segments) {
+        uint32_t count = 1;
+        const uint32_t encoding = weights.matrices[p.matrix[first]].encoding;
+        while (first + count < p.segments && weights.matrices[p.matrix[first + count]].encoding == encoding) {
+            ++count;
         }
-        check_hip(hipMalloc(reinterpret_cast<void**>(&weights.parts), needed), "projection scratch");
-        weights.parts_bytes = needed;
+        launch_run(weights, p, first, count, input, output);
+        first += count;
     }
-    args.parts = weights.parts;
-    args.partials = reinterpret_cast<float*>(weights.parts);
-    check_hip(launch_projection(Launch{weights.stream, nullptr, nullptr}, args, tiles), "projection");
 }
 
 }  // namespace
@@ -224,7 +265,15 @@ int32_t synapse_kv_weights_create(const uint8_t* blob, uint64_t blob_bytes, cons
     if (blob == nullptr || matrices == nullptr || weights == nullptr) {
         return record(SYNAPSE_KV_NULL_POINTER, "null pointer: blob, matrices or output");
     }
-    return guarded([&] { create_weights(blob, blob_bytes, matrices, count, weights); });
+    return guarded([&] { create_weights(blob, blob_bytes, matrices, nullptr, count, weights); });
+}
+
+int32_t synapse_kv_weights_create_encoded(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMatrix* matrices,
+                                          const uint32_t* encodings, uint32_t count, SynapseKvWeights** weights) {
+    if (blob == nullptr || matrices == nullptr || weights == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: blob, matrices or output");
+    }
+    return guarded([&] { create_weights(blob, blob_bytes, matrices, encodings, count, weights); });
 }
 
 void synapse_kv_weights_destroy(SynapseKvWeights* weights) { delete weights; }
@@ -259,6 +308,10 @@ int32_t synapse_kv_weights_read(SynapseKvWeights* weights, uint32_t index, uint8
             invalid("matrix " + std::to_string(index) + " of " + std::to_string(weights->matrices.size()));
         }
         const DeviceMatrix& m = weights->matrices[index];
+        if (m.encoding != kEncodingQ8_0) {
+            fail(SYNAPSE_KV_UNAVAILABLE, "matrix " + std::to_string(index) +
+                                             " is a K-quant matrix; read-back returns Q8_0 blocks only");
+        }
         const uint64_t needed = static_cast<uint64_t>(m.rows) * (m.columns / kQ8BlockElements) * kQ8BlockBytes;
         if (bytes < needed) {
             invalid("the matrix needs " + std::to_string(needed) + " bytes");

@@ -6,8 +6,9 @@ ffi.rs:106-271): it describes the mapped weights by byte offset (``DecoderDesc``
 decoder.rs:60-116), hands over the RoPE tables, and runs batched steps of ``BatchToken`` rows that return the
 logits of the tokens that ask for them. There is no CPU fallback: without the HIP library every call raises.
 
-``synthetic_model`` writes a model file of a given shape with Q8_0 matrices and FP32 norms and biases (random
-values of sane magnitude, for tests and benchmarks; there is no network for real checkpoints).
+``synthetic_model`` writes a model file of a given shape with Q8_0 (or, per matrix, Q4_K / Q6_K) matrices and FP32
+norms and biases (random values of sane magnitude, for tests and benchmarks; there is no network for real
+checkpoints).
 """
 
 from __future__ import annotations
@@ -18,8 +19,10 @@ from dataclasses import dataclass
 import numpy as np
 
 from .kv_cache import batch_tokens, rope_table
+from .projection import Q4_K_BYTES, Q6_K_BYTES, dequantize_q4_k, dequantize_q6_k, matrix_bytes
 from .native import (
-    ALL_Q8_0,
+    ENCODING_Q4_K,
+    ENCODING_Q6_K,
     ENCODING_Q8_0,
     KV_F16,
     KV_F32,
@@ -63,10 +66,48 @@ def q8_bytes(rows: int, columns: int) -> int:
     return rows * (columns // BLOCK_ELEMENTS) * BLOCK_BYTES
 
 
-def synthetic_model(shape: DecoderShape, seed: int = 0, biases: bool = True) -> tuple[np.ndarray, dict]:
+# The packing order of DecoderLayerOffsets.encodings (decoder/encoding.rs:75-85) by GGUF tensor name.
+LAYER_MATRICES = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+def q4_k_m(tensor: str) -> int:
+    """The Q4_K_M mix of the reference's K-quant tests (KQuantWeightTests.Q4KM): Q6_K for V, the feed-forward down
+    projection and the output matrix, Q4_K for the rest (the token embedding included)."""
+    return ENCODING_Q6_K if tensor in ("attn_v", "ffn_down", "output") else ENCODING_Q4_K
+
+
+def _random_kquant(rng, encoding: int, rows: int, columns: int, spread: float) -> np.ndarray:
+    """Random K-quant super-blocks with weights of standard deviation about `spread`: random code and scale bytes,
+    d (and dmin = 7.5 d for Q4_K, centring the sub-blocks on average) fitted on a sample of the blocks."""
+    per = Q4_K_BYTES if encoding == ENCODING_Q4_K else Q6_K_BYTES
+    count = rows * (columns // 256)
+    blocks = np.frombuffer(rng.bytes(count * per), dtype=np.uint8).reshape(count, per).copy()
+    def half(value: float) -> np.ndarray:
+        return np.array([value], dtype=np.float16).view(np.uint8)
+
+    one = half(1.0)
+    sample = min(count, 2048)
+    if encoding == ENCODING_Q4_K:
+        blocks[:, 0:2] = one
+        blocks[:, 2:4] = half(7.5)
+        unit = dequantize_q4_k(blocks[:sample], 256).std()
+        factor = spread / max(float(unit), 1e-30)
+        blocks[:, 0:2] = half(factor)
+        blocks[:, 2:4] = half(7.5 * factor)
+    else:
+        blocks[:, 208:210] = one
+        unit = dequantize_q6_k(blocks[:sample], 256).std()
+        blocks[:, 208:210] = half(spread / max(float(unit), 1e-30))
+    return blocks.reshape(-1)
+
+
+def synthetic_model(shape: DecoderShape, seed: int = 0, biases: bool = True, encodings=None) -> tuple[np.ndarray, dict]:
     """A model file: Q8_0 matrices (random codes, FP16 scales giving weights of standard deviation about
-    1/sqrt(columns)), FP32 norms near 1 and small FP32 biases. Returns (bytes, layout) where layout holds the byte
-    offsets in DecoderDesc / DecoderLayerOffsets terms."""
+    1/sqrt(columns)), FP32 norms near 1 and small FP32 biases. ``encodings`` (a function of the GGUF tensor name:
+    token_embd, attn_q, ..., ffn_down, output; e.g. ``q4_k_m``) picks another encoding per matrix, whose rows are
+    random K-quant super-blocks of the same spread. Returns (bytes, layout) where layout holds the byte offsets in
+    DecoderDesc / DecoderLayerOffsets terms."""
+    choose = encodings or (lambda name: ENCODING_Q8_0)
     rng = np.random.default_rng(seed)
     parts: list[tuple[str, int, object]] = []
     offset = 0
@@ -78,9 +119,10 @@ def synthetic_model(shape: DecoderShape, seed: int = 0, biases: bool = True) -> 
         offset += size
         return start
 
-    def matrix(rows: int, columns: int, spread: float) -> int:
-        start = place(q8_bytes(rows, columns), 4)
-        parts.append(("q8", start, (rows, columns, spread)))
+    def matrix(rows: int, columns: int, spread: float, name: str) -> int:
+        encoding = choose(name)
+        start = place(matrix_bytes(encoding, rows, columns), 4)
+        parts.append(("q8" if encoding == ENCODING_Q8_0 else encoding, start, (rows, columns, spread)))
         return start
 
     def vector(values: int, center: float, spread: float) -> int:
@@ -89,34 +131,40 @@ def synthetic_model(shape: DecoderShape, seed: int = 0, biases: bool = True) -> 
         return start
 
     s = shape
-    layout = {"token_embedding": matrix(s.vocabulary, s.hidden, 1.0), "layers": []}
+    layout = {"token_embedding": matrix(s.vocabulary, s.hidden, 1.0, "token_embd"), "layers": [],
+              "embedding_encoding": choose("token_embd"), "output_encoding": choose("output")}
+    packed = sum(choose(name) << (4 * index) for index, name in enumerate(LAYER_MATRICES))
     for _ in range(s.layers):
         layer = {
             "attention_norm": vector(s.hidden, 1.0, 0.2),
-            "query": matrix(s.hidden, s.hidden, s.hidden ** -0.5),
-            "key": matrix(s.kv_width, s.hidden, s.hidden ** -0.5),
-            "value": matrix(s.kv_width, s.hidden, s.hidden ** -0.5),
+            "query": matrix(s.hidden, s.hidden, s.hidden ** -0.5, "attn_q"),
+            "key": matrix(s.kv_width, s.hidden, s.hidden ** -0.5, "attn_k"),
+            "value": matrix(s.kv_width, s.hidden, s.hidden ** -0.5, "attn_v"),
             "query_bias": vector(s.hidden, 0.0, 0.1) if biases else NO_TENSOR,
             "key_bias": vector(s.kv_width, 0.0, 0.1) if biases else NO_TENSOR,
             "value_bias": vector(s.kv_width, 0.0, 0.1) if biases else NO_TENSOR,
             "query_norm": NO_TENSOR,
             "key_norm": NO_TENSOR,
-            "attention_output": matrix(s.hidden, s.hidden, s.hidden ** -0.5),
+            "attention_output": matrix(s.hidden, s.hidden, s.hidden ** -0.5, "attn_output"),
             "feed_forward_norm": vector(s.hidden, 1.0, 0.2),
-            "gate": matrix(s.feed_forward, s.hidden, s.hidden ** -0.5),
-            "up": matrix(s.feed_forward, s.hidden, s.hidden ** -0.5),
-            "down": matrix(s.hidden, s.feed_forward, s.feed_forward ** -0.5),
-            "encodings": ALL_Q8_0,
+            "gate": matrix(s.feed_forward, s.hidden, s.hidden ** -0.5, "ffn_gate"),
+            "up": matrix(s.feed_forward, s.hidden, s.hidden ** -0.5, "ffn_up"),
+            "down": matrix(s.hidden, s.feed_forward, s.feed_forward ** -0.5, "ffn_down"),
+            "encodings": packed,
         }
         layout["layers"].append(layer)
     layout["output_norm"] = vector(s.hidden, 1.0, 0.2)
-    layout["output"] = matrix(s.vocabulary, s.hidden, s.hidden ** -0.5)
+    layout["output"] = matrix(s.vocabulary, s.hidden, s.hidden ** -0.5, "output")
     blob = np.zeros(offset, dtype=np.uint8)
     for kind, start, spec in parts:
         if kind == "f32":
             values, center, spread = spec
             data = (center + spread * (rng.random(values, dtype=np.float32) * 2 - 1)).astype(np.float32)
             blob[start:start + values * 4] = data.view(np.uint8)
+        elif kind != "q8":
+            rows, columns, spread = spec
+            data = _random_kquant(rng, kind, rows, columns, spread)
+            blob[start:start + data.size] = data
         else:
             rows, columns, spread = spec
             blocks = rows * (columns // BLOCK_ELEMENTS)

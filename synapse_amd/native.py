@@ -16,7 +16,7 @@ import ctypes
 import threading
 from pathlib import Path
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 LIBRARY_PATH = Path(__file__).resolve().parent / "_lib" / "libsynapse_kv.so"
 
 STATUS_OK = 0
@@ -160,6 +160,8 @@ class PageActivation(ctypes.Structure):
 
 NO_TENSOR = (1 << 64) - 1
 ENCODING_Q8_0 = 8
+ENCODING_Q4_K = 12
+ENCODING_Q6_K = 14
 ALL_Q8_0 = 0x08888888
 
 
@@ -254,6 +256,8 @@ EXPORTS = {
     "synapse_kv_read_kv": (_I32, [_P, _U32, _U32, _U32, _U32, _P, _P]),
     "synapse_kv_rope_table": (_I32, [_U32, ctypes.c_float, ctypes.c_float, _U32, _U32, _P, _P]),
     "synapse_kv_weights_create": (_I32, [_P, _U64, ctypes.POINTER(Matrix), _U32, ctypes.POINTER(_P)]),
+    "synapse_kv_weights_create_encoded": (_I32, [_P, _U64, ctypes.POINTER(Matrix), ctypes.POINTER(_U32), _U32,
+                                                 ctypes.POINTER(_P)]),
     "synapse_kv_weights_destroy": (None, [_P]),
     "synapse_kv_weights_bytes": (_U64, [_P]),
     "synapse_kv_weights_set_stream": (_I32, [_P, _P]),

@@ -358,7 +358,8 @@ class DecoderOracle:
         self.sines = np.ascontiguousarray(sines, dtype=np.float32)
         self.layers = np.array([[int(layer[name]) for name in LAYER_FIELDS] for layer in layout["layers"]],
                                dtype=np.uint64)
-        self.top = np.array([layout["token_embedding"], layout["output_norm"], layout["output"]], dtype=np.uint64)
+        self.top = np.array([layout["token_embedding"], layout["output_norm"], layout["output"],
+                             layout.get("embedding_encoding", 8), layout.get("output_encoding", 8)], dtype=np.uint64)
         pages = max_pages or shape.session_slots * -(-shape.context // page_tokens)
         precision = 1 if shape.kv_precision in ("f16", "fp16") else 0
         self.dims = np.array([shape.layers, shape.hidden, shape.feed_forward, shape.heads, shape.kv_heads,

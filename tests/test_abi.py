@@ -41,7 +41,7 @@ def test_header_compiles_with_pinned_sizes(compiler, flag, tmp_path):
 def test_abi_version_and_struct_sizes(native):
     from synapse_amd.native import ABI_VERSION, STRUCT_SIZES
 
-    assert native.c_abi_version() == ABI_VERSION == 3
+    assert native.c_abi_version() == ABI_VERSION == 4
     for struct, size in STRUCT_SIZES.items():
         assert ctypes.sizeof(struct) == size
 
@@ -172,7 +172,8 @@ def decoder_desc(**overrides):
 
 
 @pytest.mark.parametrize("overrides,status,message", [
-    ({"output_encoding": 12}, 3, "K-quant"),
+    ({"output_encoding": 12}, 3, "tensor output has 128 columns, not a multiple of its 256-value blocks"),
+    ({"output_encoding": 14}, 3, "256-value blocks"),
     ({"embedding_encoding": 2}, 3, "not GGML type 2"),
     ({"rope_layout": 2}, 3, "NeoX RoPE"),
     ({"activation": 1}, 3, "SwiGLU"),
@@ -184,7 +185,8 @@ def decoder_desc(**overrides):
     ({"output": 10**9}, 2, "tensor output"),
     ({"output_norm": 2}, 2, "tensor output_norm"),
     ({"layer": {"query_norm": 0}}, 3, "query/key normalization"),
-    ({"layer": {"encodings": 0x08888C88}}, 3, "K-quant"),
+    ({"layer": {"encodings": 0x08888C88}}, 3, "tensor attn_v has 128 columns"),
+    ({"layer": {"encodings": 0x08888388}}, 3, "not GGML type 3"),
     ({"layer": {"key_bias": 10**9}}, 2, "layer 0: tensor attn_k.bias"),
     ({"layer": {"gate": 1}}, 2, "layer 0: tensor ffn_gate"),
 ])
@@ -195,6 +197,29 @@ def test_decoder_create_validates_the_description_first(native, overrides, statu
     assert native.c_decoder_create(ctypes.byref(desc), 0, ctypes.byref(handle)) == status
     assert message in native.last_error()
     assert not handle.value
+
+
+def test_encoded_weights_validate_before_device_work(native):
+    """synapse_kv_weights_create_encoded checks every matrix (encoding, whole blocks, range) before any HIP call."""
+    from synapse_amd.native import Matrix
+
+    blob = np.zeros(4096, dtype=np.uint8)
+    matrices = (Matrix * 1)()
+    matrices[0].weight = 0
+    matrices[0].bias = (1 << 64) - 1
+    handle = ctypes.c_void_p()
+    for encoding, rows, columns, status, message in ((3, 4, 256, 3, "not GGML type 3"),
+                                                     (12, 4, 128, 2, "multiple of 256"),
+                                                     (14, 10, 512, 2, "extend past the blob"),
+                                                     (12, 8, 1024, 2, "extend past the blob")):
+        matrices[0].rows = rows
+        matrices[0].columns = columns
+        ids = (ctypes.c_uint32 * 1)(encoding)
+        assert native.c_weights_create_encoded(blob.ctypes.data, blob.nbytes, matrices, ids, 1,
+                                               ctypes.byref(handle)) == status
+        assert message in native.last_error()
+        assert not handle.value
+    assert native.c_weights_create_encoded(None, 0, None, None, 0, None) == 1
 
 
 def test_decoder_null_pointers(native):

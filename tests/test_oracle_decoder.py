@@ -9,8 +9,8 @@ import numpy as np
 import pytest
 
 from oracle_ffi import DecoderOracle
-from synapse_amd.decoder import DecoderShape, synthetic_model
-from synapse_amd.projection import dequantize_q8_0
+from synapse_amd.decoder import LAYER_MATRICES, DecoderShape, q4_k_m, synthetic_model
+from synapse_amd.projection import dequantize, dequantize_q8_0, matrix_bytes
 
 TINY = DecoderShape(layers=2, hidden=128, feed_forward=256, heads=2, kv_heads=1, head_dim=64, vocabulary=96,
                     context=256, session_slots=3, step_tokens=16, logits_rows=8, growth=64)
@@ -33,9 +33,9 @@ class NumpyDecoder:
         self.cos = cosines.astype(np.float64)
         self.sin = sines.astype(np.float64)
 
-        def matrix(offset, rows, columns):
-            size = rows * (columns // 32) * 34
-            return dequantize_q8_0(blob[offset:offset + size], columns).astype(np.float64)
+        def matrix(offset, rows, columns, encoding=8):
+            size = matrix_bytes(encoding, rows, columns)
+            return dequantize(encoding, blob[offset:offset + size], columns).astype(np.float64)
 
         def vector(offset, count):
             if offset == (1 << 64) - 1:
@@ -43,21 +43,23 @@ class NumpyDecoder:
             return blob[offset:offset + 4 * count].view(np.float32).astype(np.float64)
 
         kv = s.kv_width
-        self.embedding = matrix(layout["token_embedding"], s.vocabulary, s.hidden)
-        self.output = matrix(layout["output"], s.vocabulary, s.hidden)
+        self.embedding = matrix(layout["token_embedding"], s.vocabulary, s.hidden, layout.get("embedding_encoding", 8))
+        self.output = matrix(layout["output"], s.vocabulary, s.hidden, layout.get("output_encoding", 8))
         self.output_norm = vector(layout["output_norm"], s.hidden)
         self.layers = []
         for layer in layout["layers"]:
+            enc = {name: (int(layer["encodings"]) >> (4 * index)) & 0xF for index, name in enumerate(LAYER_MATRICES)}
             self.layers.append({
                 "attention_norm": vector(layer["attention_norm"], s.hidden),
-                "q": matrix(layer["query"], s.hidden, s.hidden), "qb": vector(layer["query_bias"], s.hidden),
-                "k": matrix(layer["key"], kv, s.hidden), "kb": vector(layer["key_bias"], kv),
-                "v": matrix(layer["value"], kv, s.hidden), "vb": vector(layer["value_bias"], kv),
-                "o": matrix(layer["attention_output"], s.hidden, s.hidden),
+                "q": matrix(layer["query"], s.hidden, s.hidden, enc["attn_q"]),
+                "qb": vector(layer["query_bias"], s.hidden),
+                "k": matrix(layer["key"], kv, s.hidden, enc["attn_k"]), "kb": vector(layer["key_bias"], kv),
+                "v": matrix(layer["value"], kv, s.hidden, enc["attn_v"]), "vb": vector(layer["value_bias"], kv),
+                "o": matrix(layer["attention_output"], s.hidden, s.hidden, enc["attn_output"]),
                 "ffn_norm": vector(layer["feed_forward_norm"], s.hidden),
-                "gate": matrix(layer["gate"], s.feed_forward, s.hidden),
-                "up": matrix(layer["up"], s.feed_forward, s.hidden),
-                "down": matrix(layer["down"], s.hidden, s.feed_forward),
+                "gate": matrix(layer["gate"], s.feed_forward, s.hidden, enc["ffn_gate"]),
+                "up": matrix(layer["up"], s.feed_forward, s.hidden, enc["ffn_up"]),
+                "down": matrix(layer["down"], s.hidden, s.feed_forward, enc["ffn_down"]),
             })
         self.keys = {}    # (slot, layer) -> {position: [kv_heads, head_dim]}
         self.values = {}
@@ -116,14 +118,22 @@ def steps_for(rng, shape):
     return [a, b, c]
 
 
-@pytest.mark.parametrize("biases", [True, False])
-def test_oracle_decoder_matches_fp64_numpy(biases):
+# K-quant matrices need whole 256-value super-blocks: hidden and feed-forward widths of 256 and 512.
+TINY_K = DecoderShape(layers=2, hidden=256, feed_forward=512, heads=4, kv_heads=1, head_dim=64, vocabulary=96,
+                      context=256, session_slots=3, step_tokens=16, logits_rows=8, growth=64)
+
+
+@pytest.mark.parametrize("biases,encodings", [(True, None), (False, None), (True, "q4_k_m"), (False, "q6_k")])
+def test_oracle_decoder_matches_fp64_numpy(biases, encodings):
+    """Q8_0 models and K-quant ones (the Q4_K_M mix: Q4_K with Q6_K for V, down and output; and all Q6_K)."""
     rng = np.random.default_rng(3 + biases)
-    blob, layout = synthetic_model(TINY, seed=7 + biases, biases=biases)
-    cos, sin = rope_tables(TINY.head_dim, TINY.theta, TINY.context)
-    oracle = DecoderOracle(blob, layout, TINY, cos, sin)
-    reference = NumpyDecoder(blob, layout, TINY, cos, sin)
-    for step in steps_for(rng, TINY):
+    shape = TINY if encodings is None else TINY_K
+    choose = {None: None, "q4_k_m": q4_k_m, "q6_k": lambda name: 14}[encodings]
+    blob, layout = synthetic_model(shape, seed=7 + biases, biases=biases, encodings=choose)
+    cos, sin = rope_tables(shape.head_dim, shape.theta, shape.context)
+    oracle = DecoderOracle(blob, layout, shape, cos, sin)
+    reference = NumpyDecoder(blob, layout, shape, cos, sin)
+    for step in steps_for(rng, shape):
         got = oracle.forward(step)
         expected = reference.forward(step)
         assert got.shape == expected.shape
