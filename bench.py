@@ -576,8 +576,12 @@ def config_decoder(args, torch) -> dict:
     of every attended position, the new K/V, the embedding rows and the logits written."""
     import ctypes
 
-    from synapse_amd.decoder import Decoder, DecoderShape, q8_bytes, synthetic_model
+    from synapse_amd.decoder import Decoder, DecoderShape, q4_k_m, synthetic_model
     from synapse_amd.kv_cache import batch_tokens
+    from synapse_amd.projection import matrix_bytes
+
+    mix = args.weights
+    choose = q4_k_m if mix == "q4_k_m" else (lambda name: 8)
 
     lengths = lengths_for(SEED + CONFIG_OFFSET)
     total = args.warmup + args.steps
@@ -586,9 +590,10 @@ def config_decoder(args, torch) -> dict:
                          head_dim=HEAD_DIM, vocabulary=152064, context=context, session_slots=SEQUENCES,
                          step_tokens=4096, logits_rows=SEQUENCES, kv_precision="f16", growth=GROWTH)
     started = time.perf_counter()
-    blob, layout = synthetic_model(shape, seed=SEED + 8)
+    blob, layout = synthetic_model(shape, seed=SEED + 8, encodings=choose)
     model = Decoder(blob, layout, shape)
     log(f"model {blob.nbytes / 2**30:.2f} GiB built and uploaded in {time.perf_counter() - started:.1f} s")
+    del blob
     library = model.library
     cache = model.cache
     generator = torch.Generator(device="cuda")
@@ -627,21 +632,29 @@ def config_decoder(args, torch) -> dict:
     seconds = elapsed / args.steps
     s = shape
     kv = s.kv_width
-    weight_bytes = s.layers * (q8_bytes(s.hidden + 2 * kv, s.hidden) + q8_bytes(s.hidden, s.hidden) +
-                               2 * q8_bytes(s.feed_forward, s.hidden) + q8_bytes(s.hidden, s.feed_forward)) + \
-        q8_bytes(s.vocabulary, s.hidden)
+    # Bytes of the matrices in their GGML encodings (the K-quants are read from a repacked form holding 4-bit (Q4_K)
+    # or 8-bit (Q6_K) codes plus FP32 factors, more than these bytes; the roofline counts the model's own size).
+    weight_bytes = s.layers * (matrix_bytes(choose("attn_q"), s.hidden, s.hidden) +
+                               matrix_bytes(choose("attn_k"), kv, s.hidden) +
+                               matrix_bytes(choose("attn_v"), kv, s.hidden) +
+                               matrix_bytes(choose("attn_output"), s.hidden, s.hidden) +
+                               matrix_bytes(choose("ffn_gate"), s.feed_forward, s.hidden) +
+                               matrix_bytes(choose("ffn_up"), s.feed_forward, s.hidden) +
+                               matrix_bytes(choose("ffn_down"), s.hidden, s.feed_forward)) + \
+        matrix_bytes(choose("output"), s.vocabulary, s.hidden)
     keys = float(np.mean([(lengths + args.warmup + i + 1).sum() for i in range(args.steps)]))
     kv_bytes = keys * KV_BYTES_PER_TOKEN_LAYER * LAYERS + SEQUENCES * KV_BYTES_PER_TOKEN_LAYER * LAYERS
-    other = SEQUENCES * (q8_bytes(1, s.hidden) + s.vocabulary * 4)
+    other = SEQUENCES * (matrix_bytes(choose("token_embd"), 1, s.hidden) + s.vocabulary * 4)
     step_bytes = weight_bytes + kv_bytes + other
     model.close()
     achieved = step_bytes / seconds / 1e9
     return {
-        "metric": "decoder step tokens/s (embedding, 28 layers, logits), 7B-shaped Q8_0, 16 sequences @ C3 lengths",
+        "metric": f"decoder step tokens/s (embedding, 28 layers, logits), 7B-shaped {mix.upper()}, 16 sequences @ C3 "
+                  "lengths",
         "value": round(SEQUENCES / seconds, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(seconds * 1e3, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32 (Q8_0 weights, FP16 KV)",
-        "data": f"synthetic Q8_0 model (numpy seed {SEED + 8}), random K/V prefill, random token ids",
+        "vs_baseline": None, "dtype": f"f32 ({mix.upper()} weights, FP16 KV)",
+        "data": f"synthetic {mix.upper()} model (numpy seed {SEED + 8}), random K/V prefill, random token ids",
         "config": {"workload": "decoder: Qwen2.5-7B shape (hidden 3,584, ffn 18,944, 28 q / 4 KV heads, vocab "
                                "152,064), 16 sequences decoding at lengths U[1024, 32768], logits for every token",
                    "layers": LAYERS, "lengths": lengths.tolist(), "parallelism": "single GPU"},
@@ -659,6 +672,8 @@ def main() -> None:
                         help="c3: the BASELINE metric (default); c1, c2, c4: the other decode configurations; "
                              "c5: chunked-prefill MFMA throughput; proj: the Q8_0 projections around the path; "
                              "decoder: the whole decoder step on a 7B-shaped synthetic model")
+    parser.add_argument("--weights", choices=["q8_0", "q4_k_m"], default="q8_0",
+                        help="decoder: the matrices' encodings (Q8_0, or the Q4_K_M mix of Q4_K and Q6_K)")
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--split-keys", type=int, default=None)

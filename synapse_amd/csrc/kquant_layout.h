@@ -17,9 +17,9 @@
 //     because K-quant rows are whole 256-value super-blocks;
 //   * scales are FP32, 64 per tile and chunk: [row group g = (row % 16) / 4][field][block of the chunk][row % 4].
 //     For Q4_K field 0 is the block's scale d * sc and field 1 its offset dmin * m; for Q6_K field 0 is the scale of
-//     the block's first 16 columns and field 1 that of its last 16. A lane of row group g reads its 16 values with
-//     four 16-byte loads. FP16 x 6-bit and FP16 x int8 products are exact in FP32, so these are the reference's
-//     per-block factors bit for bit.
+//     the block's first 16 columns and field 1 that of its last 16. A wave reads a tile chunk's 64 factors with
+//     one 4-byte load per lane: row group g's 16 land in the 16 lanes of that row group. FP16 x 6-bit and
+//     FP16 x int8 products are exact in FP32, so these are the reference's per-block factors bit for bit.
 #pragma once
 
 #include <stddef.h>

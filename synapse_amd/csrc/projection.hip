@@ -30,6 +30,8 @@
 // in wave order, then the bias and the residual.
 
 #include "kv_internal.h"
+#include <utility>
+
 #include "kquant_layout.h"
 #include "q8_layout.h"
 
@@ -137,12 +139,15 @@ constexpr int projection_batch() {
 }
 
 // One chunk of one 16-row tile as a lane loads it: its codes (16 bytes of int8 codes; Q4_K: 8 bytes of nibbles in
-// .xy) and the factors of its accumulator rows (Q8_0: eight FP16 scales; K-quants: sixteen FP32 factors, [field]
-// [block][row]).
+// .xy) and the factors of its accumulator rows (Q8_0: eight FP16 scales, [block][row]). K-quant factors are loaded
+// one FP32 value per lane: the chunk's 64 factors, [row group][field][block][row], so row group g's sixteen sit in
+// DPP row g (lanes 16 g .. 16 g + 15), exactly the lanes whose accumulators need them; they are broadcast within the
+// row at use (row_broadcast_factors) instead of every lane loading all sixteen.
 template <uint32_t E>
 struct ChunkWeights {
     uintx4 codes;
-    uintx4 scales[E == kEncodingQ8_0 ? 1 : 4];
+    uintx4 scales;    // Q8_0
+    uint32_t factor;  // K-quants: FP32 bits of factor `lane` of the chunk
 };
 
 // Loads chunk `tile_chunk` (tile * chunks + chunk) of a matrix for lane `lane` of row group g.
@@ -157,22 +162,23 @@ __device__ inline ChunkWeights<E> load_chunk(const uint8_t* codes, const void* s
         w.codes = __builtin_nontemporal_load(reinterpret_cast<const uintx4*>(codes + tile_chunk * kQ8TileBytes) + lane);
     }
     if constexpr (E == kEncodingQ8_0) {
-        w.scales[0] = reinterpret_cast<const uintx4*>(static_cast<const uint16_t*>(scales) + tile_chunk * kQ8TileScales)[g];
+        w.scales = reinterpret_cast<const uintx4*>(static_cast<const uint16_t*>(scales) + tile_chunk * kQ8TileScales)[g];
     } else {
-        const uintx4* factors = reinterpret_cast<const uintx4*>(static_cast<const float*>(scales) + tile_chunk * kKTileScales) + 4 * g;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w.scales[i] = factors[i];
-        }
+        w.factor = reinterpret_cast<const uint32_t*>(scales)[tile_chunk * kKTileScales + lane];
     }
     return w;
 }
 
-// FP32 factor i of a lane's factor vector. The element is copied out first: a vector element is not an object of
-// its own, and a bit cast of the element expression would read the vector's first element.
-__device__ inline float factor(uintx4 v, int i) {
-    const uint32_t bits = v[i];
-    return __builtin_bit_cast(float, bits);
+// factors[n] = the value lane 16 g + n holds, for every lane of row group g (DPP row_newbcast:n).
+template <int... N>
+__device__ inline void broadcast_each(uint32_t bits, float (&factors)[16], std::integer_sequence<int, N...>) {
+    ((factors[N] = __builtin_bit_cast(
+          float, __builtin_amdgcn_update_dpp(0, static_cast<int>(bits), 0x150 + N, 0xF, 0xF, false))),
+     ...);
+}
+
+__device__ inline void row_broadcast_factors(uint32_t bits, float (&factors)[16]) {
+    broadcast_each(bits, factors, std::make_integer_sequence<int, 16>{});
 }
 
 // The chunk's two blocks of A fragments: eight codes of one row per block, exact in bf16.
@@ -215,7 +221,7 @@ __device__ inline void multiply_chunk(const ChunkWeights<E>& w, const InputFragm
         for (int b = 0; b < 2; ++b) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const uint32_t pair = w.scales[0][2 * b + h];
+                const uint32_t pair = w.scales[2 * b + h];
                 d[b][2 * h] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair & 0xFFFF)));
                 d[b][2 * h + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> 16)));
             }
@@ -257,14 +263,16 @@ __device__ inline void multiply_chunk(const ChunkWeights<E>& w, const InputFragm
                 }
             }
         }
+        float factors[16];
+        row_broadcast_factors(w.factor, factors);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
 #pragma unroll
             for (int c = 0; c < NT; ++c) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float scale = factor(w.scales[b], i);
-                    const float offset = factor(w.scales[2 + b], i);
+                    const float scale = factors[b * 4 + i];
+                    const float offset = factors[8 + b * 4 + i];
                     acc[c][i] = __builtin_fmaf(block[b][c][i], scale, acc[c][i]);
                     acc[c][i] = __builtin_fmaf(-offset, xsum[c][b], acc[c][i]);
                 }
@@ -295,6 +303,8 @@ __device__ inline void multiply_chunk(const ChunkWeights<E>& w, const InputFragm
                 }
             }
         }
+        float factors[16];
+        row_broadcast_factors(w.factor, factors);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -303,7 +313,7 @@ __device__ inline void multiply_chunk(const ChunkWeights<E>& w, const InputFragm
                 for (int c = 0; c < NT; ++c) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        acc[c][i] = __builtin_fmaf(block[h][b][c][i], factor(w.scales[2 * h + b], i), acc[c][i]);
+                        acc[c][i] = __builtin_fmaf(block[h][b][c][i], factors[h * 8 + b * 4 + i], acc[c][i]);
                     }
                 }
             }
@@ -444,7 +454,24 @@ __global__ __launch_bounds__(projection_waves<NT>() * 64) void project_kernel(Pr
 // LDS. Each slice's 16 x 16 sums go to partial rows; reduce_kernel adds the slices in order with the bias and the
 // residual. The input is read from L2 once per workgroup instead of once per tile.
 constexpr int kDecodeSliceChunks = 8;
-constexpr int kDecodeTiles = 4;
+constexpr int kDecodeWaves = 4;
+
+// Row tiles per wave of the decode kernel: each wave streams this many tiles' codes and factors against the same
+// staged input (more bytes in flight per wave; the LDS input is read once for all of them).
+#ifndef SYNAPSE_DECODE_TPW_Q8
+#define SYNAPSE_DECODE_TPW_Q8 1
+#endif
+#ifndef SYNAPSE_DECODE_TPW_K
+#define SYNAPSE_DECODE_TPW_K 2
+#endif
+template <uint32_t E>
+constexpr int decode_tiles_per_wave() {
+    return E == kEncodingQ8_0 ? SYNAPSE_DECODE_TPW_Q8 : SYNAPSE_DECODE_TPW_K;
+}
+template <uint32_t E>
+constexpr int decode_tiles() {
+    return kDecodeWaves * decode_tiles_per_wave<E>();
+}
 
 __device__ inline int locate_tile(const ProjectionArgs& a, int tile, ProjectionSegment& seg) {
     int s = 0;
@@ -456,8 +483,9 @@ __device__ inline int locate_tile(const ProjectionArgs& a, int tile, ProjectionS
 }
 
 template <uint32_t E>
-__global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(ProjectionArgs a) {
-    constexpr int kItems = kDecodeSliceChunks * 128 / (kDecodeTiles * 64);  // split items per thread
+__global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(ProjectionArgs a) {
+    constexpr int kItems = kDecodeSliceChunks * 128 / (kDecodeWaves * 64);  // split items per thread
+    constexpr int TW = decode_tiles_per_wave<E>();
     __shared__ bf16x8 staged[kDecodeSliceChunks * kParts * 2 * 64];
     // Q4_K: per chunk, 8-column group and token, the sum of the 8 inputs.
     __shared__ float group_sums[E == kEncodingQ4K ? kDecodeSliceChunks * 8 * 16 : 1];
@@ -468,14 +496,14 @@ __global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(Proje
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;
-    const int global_tile = min(blockIdx.x * kDecodeTiles + wave, a.total_tiles - 1);
+    const int first_tile = (blockIdx.x * kDecodeWaves + wave) * TW;  // this wave's tiles: first_tile + k, k < TW
 
     // 1. This thread's input loads for the split: item = threadIdx.x + 256 j is (token item % 16, 8-column group
     //    item / 16 of the slice). Tokens past the last and columns past the matrix read nothing (zeros).
     floatx4 raw[kItems][2];
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
-        const int item = threadIdx.x + j * kDecodeTiles * 64;
+        const int item = threadIdx.x + j * kDecodeWaves * 64;
         const int t = item & 15;
         const int group = item >> 4;
         const int column = (k0 + (group >> 3)) * kQ8ChunkColumns + 8 * (group & 7);
@@ -491,19 +519,23 @@ __global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(Proje
     }
     // 2. This wave's codes and scales for the slice, issued after the input loads: loads complete in issue order,
     //    so the split below waits for the input only, while the weight stream stays in flight.
-    ProjectionSegment seg;
-    const int tile = locate_tile(a, global_tile, seg);
-    const size_t first_chunk = static_cast<size_t>(tile) * a.chunks + k0;
-    ChunkWeights<E> batch[kDecodeSliceChunks];
+    //    A tile past the last loads the last tile again.
+    ChunkWeights<E> batch[TW][kDecodeSliceChunks];
 #pragma unroll
-    for (int i = 0; i < kDecodeSliceChunks; ++i) {
-        batch[i] = load_chunk<E>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
+    for (int k = 0; k < TW; ++k) {
+        ProjectionSegment seg;
+        const int tile = locate_tile(a, min(first_tile + k, a.total_tiles - 1), seg);
+        const size_t first_chunk = static_cast<size_t>(tile) * a.chunks + k0;
+#pragma unroll
+        for (int i = 0; i < kDecodeSliceChunks; ++i) {
+            batch[k][i] = load_chunk<E>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     // 3. Split into the three bf16 parts, in B-fragment order, into LDS.
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
-        const int item = threadIdx.x + j * kDecodeTiles * 64;
+        const int item = threadIdx.x + j * kDecodeWaves * 64;
         const int t = item & 15;
         const int group = item >> 4;
         const int chunk = group >> 3;
@@ -537,7 +569,11 @@ __global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(Proje
     __syncthreads();
 
     // 4. Multiply the slice against the staged input.
-    floatx4 acc[1] = {floatx4{0.0f, 0.0f, 0.0f, 0.0f}};
+    floatx4 acc[TW][1];
+#pragma unroll
+    for (int k = 0; k < TW; ++k) {
+        acc[k][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 #pragma unroll
     for (int i = 0; i < kDecodeSliceChunks; ++i) {
         if (i < count) {
@@ -557,17 +593,22 @@ __global__ __launch_bounds__(kDecodeTiles * 64) void project_decode_kernel(Proje
                     xsum[0][b] = ((four[0] + four[16]) + four[32]) + four[48];
                 }
             }
-            multiply_chunk<E, 1>(batch[i], input, xsum, acc);
+#pragma unroll
+            for (int k = 0; k < TW; ++k) {
+                multiply_chunk<E, 1>(batch[k][i], input, xsum, acc[k]);
+            }
         }
     }
-    if (blockIdx.x * kDecodeTiles + wave >= a.total_tiles) {
-        return;  // a fourth tile past the last (it loaded the last tile again)
-    }
-    // Lane (g, t) holds rows 4 g .. + 3 of token t: partial[slice][t][16 * global_tile + 4 g + i].
+    // Lane (g, t) holds rows 4 g .. + 3 of token t: partial[slice][t][16 * tile + 4 g + i].
     const int t = lane & 15;
-    float* destination = a.partials + (static_cast<size_t>(slice) * 16 + t) * a.partial_stride +
-                         static_cast<size_t>(global_tile) * kQ8TileRows + 4 * g;
-    *reinterpret_cast<floatx4*>(destination) = acc[0];
+#pragma unroll
+    for (int k = 0; k < TW; ++k) {
+        if (first_tile + k < a.total_tiles) {
+            float* destination = a.partials + (static_cast<size_t>(slice) * 16 + t) * a.partial_stride +
+                                 static_cast<size_t>(first_tile + k) * kQ8TileRows + 4 * g;
+            *reinterpret_cast<floatx4*>(destination) = acc[k][0];
+        }
+    }
 }
 
 // output[t][out_column + row] = (accumulate ? output : 0) + (sum over slices in order) + bias, one thread per
@@ -619,16 +660,22 @@ int projection_decode_slices(int chunks) { return (chunks + kDecodeSliceChunks -
 hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles) {
     const Launch plain{launch.stream, nullptr, nullptr};
     if (args.tokens <= 16) {
-        const dim3 grid((tiles + kDecodeTiles - 1) / kDecodeTiles, args.slices);
+        const dim3 block(kDecodeWaves * 64);
         switch (args.encoding) {
             case kEncodingQ4K:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ4K>, grid, dim3(kDecodeTiles * 64), launch, args);
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ4K>,
+                                  dim3((tiles + decode_tiles<kEncodingQ4K>() - 1) / decode_tiles<kEncodingQ4K>(), args.slices),
+                                  block, launch, args);
                 break;
             case kEncodingQ6K:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ6K>, grid, dim3(kDecodeTiles * 64), launch, args);
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ6K>,
+                                  dim3((tiles + decode_tiles<kEncodingQ6K>() - 1) / decode_tiles<kEncodingQ6K>(), args.slices),
+                                  block, launch, args);
                 break;
             default:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ8_0>, grid, dim3(kDecodeTiles * 64), launch, args);
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ8_0>,
+                                  dim3((tiles + decode_tiles<kEncodingQ8_0>() - 1) / decode_tiles<kEncodingQ8_0>(), args.slices),
+                                  block, launch, args);
                 break;
         }
         const int outputs = args.tokens * tiles * kQ8TileRows;
