@@ -75,20 +75,17 @@ __global__ __launch_bounds__(256) void embed_kquant_kernel(const uint8_t* table,
 // once. The sum of squares is reduced per wave, then across the workgroup's waves in order.
 constexpr int kNormGroups = 8;
 #pragma clang fp contract(off)
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float* input, const int32_t* gather, const float* weight,
-                                                       uint32_t columns, float epsilon, float* output) {
+// y = x * (1 / sqrt(mean(x^2) + eps)) * w for one row held by the workgroup (256 threads), columns 4 j' apart:
+// thread i holds float4 groups i + 256 j (zeros past the row).
+__device__ inline void normalize_row(const float4 (&values)[kNormGroups], const float* weight, uint32_t columns,
+                                     float epsilon, float* y_row) {
     __shared__ float partial[4];
-    const int row = blockIdx.x;
-    const size_t source = gather != nullptr ? static_cast<size_t>(gather[row]) : static_cast<size_t>(row);
-    const float4* x = reinterpret_cast<const float4*>(input + source * columns);
     const float4* w = reinterpret_cast<const float4*>(weight);
     const uint32_t groups = columns / 4;
-    float4 values[kNormGroups];
     float4 scales[kNormGroups];
 #pragma unroll
     for (int j = 0; j < kNormGroups; ++j) {
         const uint32_t index = threadIdx.x + 256 * j;
-        values[j] = index < groups ? x[index] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         scales[j] = index < groups ? w[index] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     float sum = 0.0f;
@@ -109,16 +106,94 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* input, const
     __syncthreads();
     const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
     const float scale = 1.0f / sqrtf(total / static_cast<float>(columns) + epsilon);
-    float4* y = reinterpret_cast<float4*>(output + static_cast<size_t>(row) * columns);
+    float4* y = reinterpret_cast<float4*>(y_row);
 #pragma unroll
     for (int j = 0; j < kNormGroups; ++j) {
         const uint32_t index = threadIdx.x + 256 * j;
         if (index < groups) {
             const float4 v = values[j];
-            const float4 s = scales[j];
-            y[index] = make_float4(v.x * scale * s.x, v.y * scale * s.y, v.z * scale * s.z, v.w * scale * s.w);
+            const float4 c = scales[j];
+            y[index] = make_float4(v.x * scale * c.x, v.y * scale * c.y, v.z * scale * c.z, v.w * scale * c.w);
         }
     }
+}
+
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* input, const int32_t* gather, const float* weight,
+                                                       uint32_t columns, float epsilon, float* output) {
+    const int row = blockIdx.x;
+    const size_t source = gather != nullptr ? static_cast<size_t>(gather[row]) : static_cast<size_t>(row);
+    const float4* x = reinterpret_cast<const float4*>(input + source * columns);
+    const uint32_t groups = columns / 4;
+    float4 values[kNormGroups];
+#pragma unroll
+    for (int j = 0; j < kNormGroups; ++j) {
+        const uint32_t index = threadIdx.x + 256 * j;
+        values[j] = index < groups ? x[index] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    normalize_row(values, weight, columns, epsilon, output + static_cast<size_t>(row) * columns);
+}
+
+// Sum over slices, in order, of a deferred projection's partial sums at `offset` (element offset of (token, row) in
+// slice 0), plus 0.0f: what reduce_kernel would have written (decode projections without biases).
+__device__ inline float slice_sum(const DeferredSums& d, size_t offset) {
+    const float* partial = d.partials + offset;
+    const size_t stride = static_cast<size_t>(16) * d.stride;
+    float sum = partial[0];
+    for (int slice = 1; slice < d.slices; ++slice) {
+        sum += partial[slice * stride];
+    }
+    return sum + 0.0f;
+}
+
+__device__ inline float4 slice_sum4(const DeferredSums& d, size_t offset) {
+    const float4* partial = reinterpret_cast<const float4*>(d.partials + offset);
+    const size_t stride = static_cast<size_t>(16) * d.stride / 4;
+    float4 sum = partial[0];
+    for (int slice = 1; slice < d.slices; ++slice) {
+        const float4 v = partial[slice * stride];
+        sum.x += v.x;
+        sum.y += v.y;
+        sum.z += v.z;
+        sum.w += v.w;
+    }
+    return make_float4(sum.x + 0.0f, sum.y + 0.0f, sum.z + 0.0f, sum.w + 0.0f);
+}
+
+// The output projection's reduce fused with the next RMS norm (one launch instead of two): hidden[t] += the
+// projection's slice sums (reduce_kernel with accumulate, in the same order), written back, then normalized into
+// `output` as rms_norm_kernel does. One workgroup per token.
+__global__ __launch_bounds__(256) void residual_norm_kernel(float* hidden, DeferredSums o, const float* weight,
+                                                            uint32_t columns, float epsilon, float* output) {
+    const int token = blockIdx.x;
+    float4* x = reinterpret_cast<float4*>(hidden + static_cast<size_t>(token) * columns);
+    const uint32_t groups = columns / 4;
+    float4 values[kNormGroups];
+#pragma unroll
+    for (int j = 0; j < kNormGroups; ++j) {
+        const uint32_t index = threadIdx.x + 256 * j;
+        values[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (index < groups) {
+            const float4 h = x[index];
+            const float4 add = slice_sum4(o, static_cast<size_t>(token) * o.stride + o.first_row[0] + 4 * index);
+            values[j] = make_float4(h.x + add.x, h.y + add.y, h.z + add.z, h.w + add.w);
+            x[index] = values[j];
+        }
+    }
+    normalize_row(values, weight, columns, epsilon, output + static_cast<size_t>(token) * columns);
+}
+
+// The gate/up projection's reduce fused with SwiGLU: gate and up are their slice sums (reduce_kernel's values), out
+// = gate / (1 + exp(-gate)) * up as swiglu_kernel computes it.
+__global__ __launch_bounds__(256) void reduce_swiglu_kernel(DeferredSums gate_up, uint32_t columns, float* output) {
+    const int token = blockIdx.y;
+    const uint32_t column = blockIdx.x * blockDim.x + threadIdx.x;
+    if (column >= columns) {
+        return;
+    }
+    const size_t row0 = static_cast<size_t>(token) * gate_up.stride;
+    const float gate = slice_sum(gate_up, row0 + gate_up.first_row[0] + column);
+    const float up = slice_sum(gate_up, row0 + gate_up.first_row[1] + column);
+    output[static_cast<size_t>(token) * columns + column] = gate / (1.0f + expf(-gate)) * up;
 }
 
 // synapse_swiglu (elementwise.cu:97-109): out = gate / (1 + exp(-gate)) * up, gate and up side by side in each row.
@@ -440,6 +515,24 @@ void project(SynapseKvDecoder& m, std::initializer_list<std::pair<uint32_t, uint
     check_status(synapse_kv_project(m.weights, &p, input, output));
 }
 
+// The same, leaving a decode projection's slice sums to the caller's next kernel (DeferredSums).
+DeferredSums project_deferred_sums(SynapseKvDecoder& m, std::initializer_list<std::pair<uint32_t, uint32_t>> parts,
+                                   uint32_t tokens, const float* input, uint32_t in_stride, float* output,
+                                   uint32_t out_stride, bool accumulate) {
+    SynapseKvProjection p{};
+    p.segments = 0;
+    for (const auto& [matrix, column] : parts) {
+        p.matrix[p.segments] = matrix;
+        p.out_column[p.segments] = column;
+        ++p.segments;
+    }
+    p.tokens = tokens;
+    p.in_stride = in_stride;
+    p.out_stride = out_stride;
+    p.accumulate = accumulate ? 1 : 0;
+    return project_deferred(*m.weights, p, input, output);
+}
+
 // DecoderPlan::validate_step (decoder.rs:303-335): returns the number of logits rows.
 uint32_t validate_step(const SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t count) {
     const SynapseKvDecoderDesc& d = m.shape;
@@ -518,14 +611,32 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
         project(m, {{base, 0}, {base + 1, hidden}, {base + 2, hidden + kv}}, n, m.normalized.pointer, hidden,
                 m.qkv.pointer, qkv_width, false);
         check_status(synapse_kv_append_attention(m.cache, layer, m.qkv.pointer, qkv_width, m.attention.pointer, hidden));
-        project(m, {{base + 3, 0}}, n, m.attention.pointer, hidden, m.hidden.pointer, hidden, true);
-        hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(256), 0, m.stream, m.hidden.pointer,
-                           static_cast<const int32_t*>(nullptr), ffn_norm, hidden, d.rms_epsilon, m.normalized.pointer);
+        // Decode steps leave the output and gate/up projections' slice sums to the kernels that consume them: the
+        // residual add runs inside the feed-forward norm and the gate/up sums inside SwiGLU (two launches fewer).
+        const DeferredSums o = project_deferred_sums(m, {{base + 3, 0}}, n, m.attention.pointer, hidden,
+                                                     m.hidden.pointer, hidden, true);
+        if (o.deferred) {
+            hipLaunchKernelGGL(residual_norm_kernel, dim3(n), dim3(256), 0, m.stream, m.hidden.pointer, o, ffn_norm,
+                               hidden, d.rms_epsilon, m.normalized.pointer);
+        } else {
+            hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(256), 0, m.stream, m.hidden.pointer,
+                               static_cast<const int32_t*>(nullptr), ffn_norm, hidden, d.rms_epsilon,
+                               m.normalized.pointer);
+        }
         check_hip(hipGetLastError(), "feed-forward norm");
-        project(m, {{base + 4, 0}, {base + 5, ffn}}, n, m.normalized.pointer, hidden, m.gate_up.pointer, 2 * ffn, false);
-        hipLaunchKernelGGL(swiglu_kernel, dim3((ffn + 255) / 256, n), dim3(256), 0, m.stream, m.gate_up.pointer, ffn,
-                           m.feed_forward.pointer);
+        const DeferredSums gate_up = project_deferred_sums(m, {{base + 4, 0}, {base + 5, ffn}}, n,
+                                                           m.normalized.pointer, hidden, m.gate_up.pointer, 2 * ffn,
+                                                           false);
+        if (gate_up.deferred) {
+            hipLaunchKernelGGL(reduce_swiglu_kernel, dim3((ffn + 255) / 256, n), dim3(256), 0, m.stream, gate_up, ffn,
+                               m.feed_forward.pointer);
+        } else {
+            hipLaunchKernelGGL(swiglu_kernel, dim3((ffn + 255) / 256, n), dim3(256), 0, m.stream, m.gate_up.pointer,
+                               ffn, m.feed_forward.pointer);
+        }
         check_hip(hipGetLastError(), "SwiGLU");
+        // The down projection's slice sums (a slice per 512 columns of 18,944: 37 at the 7B shape) are added by its
+        // own reduce: one workgroup per token reading them all in the next norm measured slower than the launch.
         project(m, {{base + 6, 0}}, n, m.feed_forward.pointer, ffn, m.hidden.pointer, hidden, true);
     }
     if (rows > 0) {

@@ -286,7 +286,8 @@ hipError_t launch_summaries(const Launch& launch, const SummaryArgs& args, bool 
 // Key-bound selection (the largest job has `most_candidates` candidates), with args.summary_count summary items.
 hipError_t launch_select(const Launch& launch, const SelectArgs& args, int most_candidates, bool fp16);
 // A projection over `tiles` row tiles (all segments); token tiles of 16 * projection_token_tiles(tokens).
-hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles);
+// `reduce` false (decode launches only): the slice sums stay in args.partials for the caller to add.
+hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles, bool reduce = true);
 int projection_token_tiles(int tokens);
 // Column slices of a decode projection (tokens <= 16) over `chunks` 64-column chunks.
 int projection_decode_slices(int chunks);
@@ -303,4 +304,23 @@ constexpr int kMergeSteps = 4;
 // Fewest 64-key steps per listed (shared-prefix) prefill item.
 constexpr int kMinSharedSteps = 4;
 
+// A decode projection (at most 16 tokens, one encoding, no biases) whose slice sums are left for the caller:
+// output[t][row of segment s] would be sum over slices, in order, of partials[(slice * 16 + t) * stride +
+// first_row[s] + row] (plus 0.0f), added to the output when accumulating. Other projections run whole and return
+// `deferred` false. The sums live in the weights' scratch until the next projection on its stream.
+struct DeferredSums {
+    const float* partials = nullptr;
+    int64_t stride = 0;
+    int32_t slices = 0;
+    int32_t first_row[3] = {0, 0, 0};
+    bool deferred = false;
+};
+
+}  // namespace synapse_kv
+
+struct SynapseKvWeights;
+
+namespace synapse_kv {
+DeferredSums project_deferred(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input,
+                              float* output);
 }  // namespace synapse_kv

@@ -653,7 +653,7 @@ int projection_token_tiles(int tokens) { return tokens <= 16 ? 1 : 4; }
 
 int projection_decode_slices(int chunks) { return (chunks + kDecodeSliceChunks - 1) / kDecodeSliceChunks; }
 
-hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles) {
+hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles, bool reduce) {
     const Launch plain{launch.stream, nullptr, nullptr};
     if (args.tokens <= 16) {
         const dim3 block(kDecodeWaves * 64);
@@ -674,8 +674,10 @@ hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, i
                                   block, launch, args);
                 break;
         }
-        const int outputs = args.tokens * tiles * kQ8TileRows;
-        SYNAPSE_KV_LAUNCH(reduce_kernel, dim3((outputs + 255) / 256), dim3(256), plain, args);
+        if (reduce) {
+            const int outputs = args.tokens * tiles * kQ8TileRows;
+            SYNAPSE_KV_LAUNCH(reduce_kernel, dim3((outputs + 255) / 256), dim3(256), plain, args);
+        }
         return hipGetLastError();
     }
     const int splits = args.tokens * (args.padded_columns / 8);

@@ -149,8 +149,8 @@ void create_weights(const uint8_t* blob, uint64_t blob_bytes, const SynapseKvMat
 }
 
 // One launch over segments [first, first + count) of the projection, which share an encoding.
-void launch_run(SynapseKvWeights& weights, const SynapseKvProjection& p, uint32_t first, uint32_t count,
-                const float* input, float* output) {
+DeferredSums launch_run(SynapseKvWeights& weights, const SynapseKvProjection& p, uint32_t first, uint32_t count,
+                        const float* input, float* output, bool reduce = true) {
     ProjectionArgs args{};
     int tiles = 0;
     uint32_t columns = 0;
@@ -205,10 +205,19 @@ void launch_run(SynapseKvWeights& weights, const SynapseKvProjection& p, uint32_
     args.sums = p.tokens > 16 && encoding == kEncodingQ4K
                     ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(weights.parts) + parts_bytes)
                     : nullptr;
-    check_hip(launch_projection(Launch{weights.stream, nullptr, nullptr}, args, tiles), "projection");
+    check_hip(launch_projection(Launch{weights.stream, nullptr, nullptr}, args, tiles, reduce), "projection");
+    DeferredSums sums;
+    sums.deferred = !reduce && p.tokens <= 16;
+    sums.partials = args.partials;
+    sums.stride = args.partial_stride;
+    sums.slices = args.slices;
+    for (uint32_t s = 0; s < count; ++s) {
+        sums.first_row[s] = args.segment[s].first_tile * kQ8TileRows;
+    }
+    return sums;
 }
 
-void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output) {
+void validate_projection(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output) {
     if (p.segments < 1 || p.segments > 3) {
         invalid("a projection has 1..3 segments");
     }
@@ -240,6 +249,10 @@ void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const floa
     check_hip(hipSetDevice(weights.device), "set device");
     check_device_pointer(weights, input, "input");
     check_device_pointer(weights, output, "output");
+}
+
+void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output) {
+    validate_projection(weights, p, input, output);
     // Consecutive segments of one encoding share a launch (the kernels are specialised per encoding).
     uint32_t first = 0;
     while (first < p.segments) {
@@ -254,6 +267,22 @@ void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const floa
 }
 
 }  // namespace
+
+DeferredSums project_deferred(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input,
+                              float* output) {
+    validate_projection(weights, p, input, output);
+    bool single = p.tokens <= 16;
+    for (uint32_t s = 0; s < p.segments; ++s) {
+        const DeviceMatrix& m = weights.matrices[p.matrix[s]];
+        single = single && !m.has_bias && m.encoding == weights.matrices[p.matrix[0]].encoding;
+    }
+    if (!single) {
+        project(weights, p, input, output);
+        return DeferredSums{};
+    }
+    return launch_run(weights, p, 0, p.segments, input, output, false);
+}
+
 }  // namespace synapse_kv
 
 using namespace synapse_kv;
