@@ -15,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "../../include/synapse_gpu.h"
 #include "abi_support.h"
 #include "kquant_layout.h"
 #include "kv_internal.h"
@@ -719,6 +720,67 @@ int32_t synapse_kv_decoder_set_stream(SynapseKvDecoder* model, void* stream) {
         synapse_kv::check_status(synapse_kv_weights_set_stream(model->weights, stream));
         model->stream = static_cast<hipStream_t>(stream);
     });
+}
+
+// ---- libsynapse_gpu's ABI version 3 (include/synapse_gpu.h; ffi.rs:12-271) for the HIP backend ----
+
+uint32_t synapse_gpu_abi_version(void) { return SYNAPSE_GPU_ABI_VERSION; }
+
+// unsupported_backend (ffi.rs:46-51): Metal exists only on macOS; this build has no CUDA either.
+static int32_t unsupported_backend(uint32_t backend) {
+    if (backend == SYNAPSE_GPU_BACKEND_METAL) {
+        return synapse_kv::record(SYNAPSE_KV_UNAVAILABLE, "the Metal backend exists only on macOS");
+    }
+    if (backend == SYNAPSE_GPU_BACKEND_CUDA) {
+        return synapse_kv::record(SYNAPSE_KV_UNAVAILABLE, "the CUDA backend is not part of this HIP build");
+    }
+    return synapse_kv::record(SYNAPSE_KV_INVALID_ARGUMENT, "invalid argument: unknown GPU backend " +
+                                                               std::to_string(backend));
+}
+
+int32_t synapse_gpu_probe(uint32_t backend, GpuDeviceInfo* info) {
+    if (info == nullptr) {
+        return synapse_kv::record(SYNAPSE_KV_NULL_POINTER, "null pointer: device info");
+    }
+    if (backend != SYNAPSE_GPU_BACKEND_HIP) {
+        return unsupported_backend(backend);
+    }
+    return synapse_kv_probe(info);
+}
+
+size_t synapse_gpu_last_error(uint8_t* buffer, size_t capacity) { return synapse_kv_last_error(buffer, capacity); }
+
+int32_t synapse_gpu_decoder_create(uint32_t backend, const DecoderDesc* desc, GpuModel** model) {
+    if (desc == nullptr || model == nullptr) {
+        return synapse_kv::record(SYNAPSE_KV_NULL_POINTER, "null pointer: model description or output");
+    }
+    // DecoderPlan::new runs before the backend is chosen (ffi.rs:122-137).
+    const int32_t status = synapse_kv::guarded([&] { synapse_kv::validate(*desc); });
+    if (status != SYNAPSE_KV_OK) {
+        return status;
+    }
+    if (backend != SYNAPSE_GPU_BACKEND_HIP) {
+        return unsupported_backend(backend);
+    }
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        (void)hipGetLastError();
+        return synapse_kv::record(SYNAPSE_KV_UNAVAILABLE, "no HIP device is available");
+    }
+    return synapse_kv_decoder_create(desc, device, model);
+}
+
+int32_t synapse_gpu_decoder_forward(GpuModel* model, const BatchToken* tokens, size_t count, float* logits,
+                                    size_t logits_capacity) {
+    return synapse_kv_decoder_forward(model, tokens, count, logits, logits_capacity);
+}
+
+void synapse_gpu_decoder_destroy(GpuModel* model) { synapse_kv_decoder_destroy(model); }
+
+uint64_t synapse_gpu_decoder_kv_bytes(const GpuModel* model) { return synapse_kv_decoder_kv_bytes(model); }
+
+int32_t synapse_gpu_decoder_reserve(GpuModel* model, uint32_t slot, uint32_t positions) {
+    return synapse_kv_decoder_reserve(model, slot, positions);
 }
 
 }  // extern "C"

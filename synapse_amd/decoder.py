@@ -180,7 +180,9 @@ class Decoder:
     """A dense decoder on the device: ``forward(tokens)`` returns the logits rows the tokens ask for."""
 
     def __init__(self, blob: np.ndarray, layout: dict, shape: DecoderShape, device: int = 0,
-                 library: NativeKvLibrary | None = None):
+                 library: NativeKvLibrary | None = None, abi: str = "kv"):
+        """``abi`` "gpu" creates and steps the model through libsynapse_gpu's ABI version 3 (synapse_gpu_*, backend
+        3 on the current device) instead of synapse_kv_decoder_*: the reference loader's own calls."""
         self.library = library or NativeKvLibrary.load()
         self.shape = shape
         self.blob = np.ascontiguousarray(blob, dtype=np.uint8)
@@ -218,7 +220,13 @@ class Decoder:
         desc.output_encoding = layout.get("output_encoding", ENCODING_Q8_0)
         self.desc = desc
         handle = ctypes.c_void_p()
-        self.library.check(self.library.c_decoder_create(ctypes.byref(desc), device, ctypes.byref(handle)))
+        self.abi = abi
+        if abi == "gpu":
+            from .native import GPU_BACKEND_HIP
+
+            self.library.check(self.library.g_decoder_create(GPU_BACKEND_HIP, ctypes.byref(desc), ctypes.byref(handle)))
+        else:
+            self.library.check(self.library.c_decoder_create(ctypes.byref(desc), device, ctypes.byref(handle)))
         self.handle = handle
         cache = ctypes.c_void_p()
         self.library.check(self.library.c_decoder_cache(self.handle, ctypes.byref(cache)))
@@ -226,7 +234,10 @@ class Decoder:
 
     def close(self) -> None:
         if getattr(self, "handle", None) is not None and self.handle.value:
-            self.library.c_decoder_destroy(self.handle)
+            if getattr(self, "abi", "kv") == "gpu":
+                self.library.g_decoder_destroy(self.handle)
+            else:
+                self.library.c_decoder_destroy(self.handle)
             self.handle = None
 
     def __del__(self):
@@ -257,7 +268,9 @@ class Decoder:
             logits = out.reshape(-1)[:max(rows, 1) * self.shape.vocabulary].reshape(max(rows, 1), -1)
         else:
             logits = np.zeros((max(rows, 1), self.shape.vocabulary), dtype=np.float32)
-        if prompt_start is None:
+        if prompt_start is None and self.abi == "gpu":
+            status = self.library.g_decoder_forward(self.handle, buffer, len(buffer), logits.ctypes.data, logits.size)
+        elif prompt_start is None:
             status = self.library.c_decoder_forward(self.handle, buffer, len(buffer), logits.ctypes.data, logits.size)
         else:
             status = self.library.c_decoder_forward_prompt(self.handle, buffer, len(buffer), prompt_start,

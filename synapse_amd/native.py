@@ -273,6 +273,22 @@ EXPORTS = {
     "synapse_kv_decoder_set_stream": (_I32, [_P, _P]),
 }
 
+# libsynapse_gpu's ABI version 3 (include/synapse_gpu.h), exported by the same library for the HIP backend.
+GPU_ABI_VERSION = 3
+GPU_BACKEND_METAL = 1
+GPU_BACKEND_CUDA = 2
+GPU_BACKEND_HIP = 3
+GPU_EXPORTS = {
+    "synapse_gpu_abi_version": (_U32, []),
+    "synapse_gpu_probe": (_I32, [_U32, ctypes.POINTER(DeviceInfo)]),
+    "synapse_gpu_last_error": (_SIZE, [ctypes.c_char_p, _SIZE]),
+    "synapse_gpu_decoder_create": (_I32, [_U32, ctypes.POINTER(DecoderDesc), ctypes.POINTER(_P)]),
+    "synapse_gpu_decoder_forward": (_I32, [_P, ctypes.POINTER(BatchToken), _SIZE, _P, _SIZE]),
+    "synapse_gpu_decoder_destroy": (None, [_P]),
+    "synapse_gpu_decoder_kv_bytes": (_U64, [_P]),
+    "synapse_gpu_decoder_reserve": (_I32, [_P, _U32, _U32]),
+}
+
 
 class NativeKvLibrary:
     """The loaded library with typed entry points and status checking."""
@@ -301,6 +317,11 @@ class NativeKvLibrary:
             function.restype = restype
             function.argtypes = argtypes
             setattr(self, "c_" + name[len("synapse_kv_"):], function)
+        for name, (restype, argtypes) in GPU_EXPORTS.items():
+            function = getattr(self.handle, name)
+            function.restype = restype
+            function.argtypes = argtypes
+            setattr(self, "g_" + name[len("synapse_gpu_"):], function)
 
     @classmethod
     def load(cls, path: Path | None = None) -> "NativeKvLibrary":

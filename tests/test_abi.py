@@ -13,6 +13,7 @@ from oracle_ffi import rope_table as oracle_rope_table
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "synapse_kv.h"
+GPU_HEADER = ROOT / "include" / "synapse_gpu.h"
 
 
 def declared_functions():
@@ -229,3 +230,54 @@ def test_decoder_null_pointers(native):
     assert native.c_decoder_kv_bytes(None) == 0
     assert native.c_decoder_cache(None, None) == 1
     native.c_decoder_destroy(None)
+
+
+# ---- libsynapse_gpu's ABI version 3 (include/synapse_gpu.h) ----
+
+def test_gpu_abi_is_declared_exported_and_versioned(native, tmp_path):
+    """The eight functions NativeGpuLibrary binds (NativeGpuLibrary.cs:49-75) are exported with ABI version 3, and
+    the header compiles in C and C++ with the reference's type names."""
+    from synapse_amd.native import GPU_ABI_VERSION, GPU_EXPORTS
+
+    declared = sorted(set(re.findall(r"^\w[\w\s\*]*?\b(synapse_gpu_\w+)\s*\(", GPU_HEADER.read_text(),
+                                     flags=re.MULTILINE)))
+    exported = subprocess.run(["nm", "-D", "--defined-only", str(native.path)], capture_output=True, text=True,
+                              check=True).stdout
+    assert set(declared) == set(re.findall(r"\b(synapse_gpu_\w+)\b", exported)) == set(GPU_EXPORTS)
+    assert len(declared) == 8
+    assert native.g_abi_version() == GPU_ABI_VERSION == 3
+    for compiler, flag, suffix in (("gcc", "-std=c11", "c"), ("g++", "-std=c++17", "cpp")):
+        source = tmp_path / f"gpu.{suffix}"
+        source.write_text('#include "synapse_gpu.h"\n'
+                          "int main(void) { return (int)(sizeof(DecoderDesc) + sizeof(DecoderLayerOffsets) +"
+                          " sizeof(BatchToken) + sizeof(GpuDeviceInfo)) - (136 + 120 + 16 + 152); }\n")
+        subprocess.run([compiler, flag, "-fsyntax-only", "-I", str(GPU_HEADER.parent), str(source)], check=True)
+
+
+def test_gpu_abi_errors_follow_ffi_rs(native):
+    """ffi.rs order: null checks, then DecoderPlan::new, then the backend (Metal and CUDA status 3 here, unknown
+    ids status 2); the last error is the thread's, shared with synapse_kv_last_error; null-safe destroy/kv_bytes."""
+    from synapse_amd.native import DeviceInfo
+
+    info = DeviceInfo()
+    assert native.g_probe(3, None) == 1
+    assert native.g_probe(1, ctypes.byref(info)) == 3 and "macOS" in native.last_error()
+    assert native.g_probe(2, ctypes.byref(info)) == 3 and "CUDA" in native.last_error()
+    assert native.g_probe(9, ctypes.byref(info)) == 2 and "unknown GPU backend 9" in native.last_error()
+    handle = ctypes.c_void_p()
+    assert native.g_decoder_create(3, None, ctypes.byref(handle)) == 1
+    desc, _keep = decoder_desc()
+    for backend, status, message in ((1, 3, "macOS"), (2, 3, "CUDA"), (7, 2, "unknown GPU backend 7")):
+        assert native.g_decoder_create(backend, ctypes.byref(desc), ctypes.byref(handle)) == status
+        assert message in native.last_error()
+        assert not handle.value
+    bad, _keep_bad = decoder_desc(rope_layout=2)
+    assert native.g_decoder_create(7, ctypes.byref(bad), ctypes.byref(handle)) == 3  # validation comes first
+    assert "NeoX RoPE" in native.last_error()
+    buffer = ctypes.create_string_buffer(256)
+    length = native.g_last_error(buffer, 256)
+    assert buffer.raw[:length].decode() == native.last_error()
+    assert native.g_decoder_forward(None, None, 0, None, 0) == 1
+    assert native.g_decoder_reserve(None, 0, 0) == 1
+    assert native.g_decoder_kv_bytes(None) == 0
+    native.g_decoder_destroy(None)

@@ -127,3 +127,28 @@ def test_decoder_with_page_activation_runs_and_differs(torch_gpu):
     spread = results[0].max() - results[0].min()
     assert np.abs(results[0] - results[1]).max() <= 1e-5 * spread
     assert np.abs(results[0] - results[2]).max() > 1e-3 * spread
+
+
+def test_decoder_through_the_libsynapse_gpu_abi(torch_gpu):
+    """The reference loader's calls (synapse_gpu_probe / _decoder_create with backend 3 / _forward / _reserve /
+    _kv_bytes / _destroy) drive the same model: logits bit-identical to synapse_kv_decoder_* on the same steps."""
+    import ctypes
+
+    from synapse_amd.native import DeviceInfo, NativeKvLibrary
+
+    say("decoder via synapse_gpu ABI")
+    library = NativeKvLibrary.load()
+    info = DeviceInfo()
+    library.check(library.g_probe(3, ctypes.byref(info)))
+    shape = SHAPES[1][1]
+    blob, layout = synthetic_model(shape, seed=11)
+    native_abi = Decoder(blob, layout, shape)
+    gpu_abi = Decoder(blob, layout, shape, abi="gpu")
+    rng = np.random.default_rng(11)
+    for tokens in steps(rng, shape)[:4]:
+        assert np.array_equal(native_abi.forward(tokens), gpu_abi.forward(tokens))
+    library.check(library.g_decoder_reserve(gpu_abi.handle, 2, 700))
+    assert library.g_decoder_kv_bytes(gpu_abi.handle) == library.c_decoder_kv_bytes(gpu_abi.handle)
+    assert library.g_decoder_kv_bytes(gpu_abi.handle) > native_abi.kv_bytes
+    native_abi.close()
+    gpu_abi.close()
