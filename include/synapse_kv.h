@@ -238,6 +238,58 @@ int32_t synapse_kv_page_stats(SynapseKvCache* cache, SynapseKvPageStats* stats);
 int32_t synapse_kv_read_kv(SynapseKvCache* cache, uint32_t slot, uint32_t layer, uint32_t first, uint32_t count,
                            void* keys, void* values);
 
+/* ---- Persistent prefix payloads (ADR-018's next step) ----
+ * A slot's first `length` positions serialized for a prefix cache outside the process: payloads keyed by model,
+ * tokenizer, RoPE, KV type and prefix hash (ADR-018-prompt-prefix-reuse.md:42-44). The library writes and checks
+ * the payload; where it is stored (the reference plans ZoneTree metadata and files on disk) is the caller's.
+ *
+ * Format, little-endian: a 128-byte SynapseKvPrefixHeader, then per layer the K rows and then the V rows of
+ * positions 0..length-1, each [length][kv_heads][head_dim] in the storage type (FP16 or FP32; K already rotated).
+ * payload_bytes counts those rows; checksum is FNV-1a 64 over them. Importing into an empty slot reproduces the
+ * K/V bytes exactly, so attention over the imported prefix equals attention over the original. */
+typedef struct SynapseKvPrefixKey {
+    uint64_t model;     /* caller's hash of the model file / weights */
+    uint64_t tokenizer; /* caller's hash of the tokenizer */
+    uint64_t rope;      /* caller's hash of the RoPE parameters (theta, scaling) */
+    uint64_t prefix;    /* synapse_kv_prefix_hash of the prefix's token ids */
+} SynapseKvPrefixKey;
+
+#define SYNAPSE_KV_PREFIX_MAGIC "SYNKVPX1"
+#define SYNAPSE_KV_PREFIX_VERSION 1u
+
+typedef struct SynapseKvPrefixHeader {
+    char magic[8];           /* SYNAPSE_KV_PREFIX_MAGIC, not terminated */
+    uint32_t version;        /* SYNAPSE_KV_PREFIX_VERSION */
+    uint32_t header_bytes;   /* 128 */
+    SynapseKvPrefixKey key;  /* the KV type and shape are checked from the fields below */
+    uint32_t kv_precision;   /* SYNAPSE_KV_F32 or SYNAPSE_KV_F16 */
+    uint32_t layer_count;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t length;         /* positions stored */
+    uint32_t reserved0;      /* 0 */
+    uint64_t payload_bytes;  /* 2 * layer_count * length * kv_heads * head_dim * element bytes */
+    uint64_t checksum;       /* FNV-1a 64 of the payload */
+    uint8_t reserved[40];    /* 0 */
+} SynapseKvPrefixHeader;
+
+/* FNV-1a 64 (offset basis 0xcbf29ce484222325, prime 0x100000001b3) of `count` bytes: the prefix hash of a token
+ * list is this over its int32 ids in little-endian order. */
+uint64_t synapse_kv_prefix_hash(const uint8_t* bytes, size_t count);
+
+/* Writes slot `slot`'s positions 0..length-1 (length at most the slot's written length) as a payload keyed by
+ * `key` into `payload` (`capacity` bytes) and stores its size in `*bytes`. A null `payload` only reports the
+ * size. Synchronizes the cache's stream. */
+int32_t synapse_kv_export_prefix(SynapseKvCache* cache, uint32_t slot, uint32_t length, const SynapseKvPrefixKey* key,
+                                 uint8_t* payload, uint64_t capacity, uint64_t* bytes);
+
+/* Loads a payload into the empty slot `slot`: checks the magic, version, sizes, checksum, the cache's KV type and
+ * shape, and that the payload's key equals `key` (status 2 otherwise, the slot untouched); reserves the slot with
+ * the capacity policy, writes the K/V rows and sets the written length, stored in `*length`. Key summaries of
+ * KV page activation are recomputed for the imported blocks. */
+int32_t synapse_kv_import_prefix(SynapseKvCache* cache, uint32_t slot, const SynapseKvPrefixKey* key,
+                                 const uint8_t* payload, uint64_t bytes, uint32_t* length);
+
 /* RopeFrequencies (RopeFrequencies.cs:20-81) into host [positions][head_dim / 2] tables; yarn_factor <= 0 means
  * unscaled. The C# host builds the same tables itself (GpuDecoderExecutor.BuildRopeTables,
  * GpuDecoderExecutor.cs:183-192). */
@@ -422,6 +474,8 @@ static_assert(sizeof(SynapseKvPageActivation) == 24, "SynapseKvPageActivation is
 static_assert(sizeof(SynapseKvProjection) == 48, "SynapseKvProjection is pinned at 48 bytes");
 static_assert(sizeof(SynapseKvLayerOffsets) == 120, "SynapseKvLayerOffsets is pinned at 120 bytes");
 static_assert(sizeof(SynapseKvDecoderDesc) == 136, "SynapseKvDecoderDesc is pinned at 136 bytes");
+static_assert(sizeof(SynapseKvPrefixKey) == 32, "SynapseKvPrefixKey is pinned at 32 bytes");
+static_assert(sizeof(SynapseKvPrefixHeader) == 128, "SynapseKvPrefixHeader is pinned at 128 bytes");
 #else
 _Static_assert(sizeof(SynapseKvDeviceInfo) == 152, "SynapseKvDeviceInfo is pinned at 152 bytes");
 _Static_assert(sizeof(SynapseKvBatchToken) == 16, "SynapseKvBatchToken is pinned at 16 bytes");
@@ -433,6 +487,8 @@ _Static_assert(sizeof(SynapseKvPageActivation) == 24, "SynapseKvPageActivation i
 _Static_assert(sizeof(SynapseKvProjection) == 48, "SynapseKvProjection is pinned at 48 bytes");
 _Static_assert(sizeof(SynapseKvLayerOffsets) == 120, "SynapseKvLayerOffsets is pinned at 120 bytes");
 _Static_assert(sizeof(SynapseKvDecoderDesc) == 136, "SynapseKvDecoderDesc is pinned at 136 bytes");
+_Static_assert(sizeof(SynapseKvPrefixKey) == 32, "SynapseKvPrefixKey is pinned at 32 bytes");
+_Static_assert(sizeof(SynapseKvPrefixHeader) == 128, "SynapseKvPrefixHeader is pinned at 128 bytes");
 #endif
 
 #endif /* SYNAPSE_KV_H */

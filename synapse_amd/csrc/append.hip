@@ -124,6 +124,30 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     }
 }
 
+// The inverse of gather_kernel: rows [count][kv_heads][head_dim] of K and V (the storage type) written into
+// positions first.. of one slot and layer (prefix import).
+template <typename T>
+__global__ __launch_bounds__(256) void scatter_kernel(GatherArgs a) {
+    const Geometry& g = a.geo;
+    const int d = g.head_dim;
+    const size_t per_position = static_cast<size_t>(g.kv_heads) * d;
+    const size_t total = per_position * a.count;
+    const size_t region = static_cast<size_t>(g.page_tokens) * d;
+    const size_t layer_base = static_cast<size_t>(g.layer) * 2 * g.kv_heads;
+    for (size_t index = blockIdx.x * 256ull + threadIdx.x; index < total; index += gridDim.x * 256ull) {
+        const int position = a.first + static_cast<int>(index / per_position);
+        const int kv_head = static_cast<int>((index % per_position) / d);
+        const int dim = static_cast<int>(index % d);
+        const int logical = position / g.page_tokens;
+        const int within = position - logical * g.page_tokens;
+        const int page = g.block_table[static_cast<size_t>(a.slot) * g.pages_per_slot + logical];
+        T* base = reinterpret_cast<T*>(const_cast<uint8_t*>(g.pool) + static_cast<uint64_t>(page) * g.page_bytes);
+        base[(layer_base + kv_head) * region + key_offset<T>(d, within, dim)] = reinterpret_cast<const T*>(a.keys)[index];
+        base[(layer_base + g.kv_heads + kv_head) * region + value_offset<T>(d, within, dim)] =
+            reinterpret_cast<const T*>(a.values)[index];
+    }
+}
+
 }  // namespace
 
 hipError_t launch_append(const Launch& launch, const AppendArgs& args, int tokens, bool fp16) {
@@ -149,6 +173,21 @@ hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16
         SYNAPSE_KV_LAUNCH(gather_kernel<_Float16>, grid, dim3(256), launch, args);
     } else {
         SYNAPSE_KV_LAUNCH(gather_kernel<float>, grid, dim3(256), launch, args);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_scatter(const Launch& launch, const GatherArgs& args, bool fp16) {
+    const size_t total = static_cast<size_t>(args.geo.kv_heads) * args.geo.head_dim * args.count;
+    if (total == 0) {
+        return hipSuccess;
+    }
+    const size_t blocks = (total + 255) / 256;
+    const dim3 grid(static_cast<unsigned>(blocks < 4096 ? blocks : 4096));
+    if (fp16) {
+        SYNAPSE_KV_LAUNCH(scatter_kernel<_Float16>, grid, dim3(256), launch, args);
+    } else {
+        SYNAPSE_KV_LAUNCH(scatter_kernel<float>, grid, dim3(256), launch, args);
     }
     return hipGetLastError();
 }

@@ -1867,6 +1867,203 @@ int32_t synapse_kv_read_kv(SynapseKvCache* cache, uint32_t slot, uint32_t layer,
     });
 }
 
+// ---- Persistent prefix payloads ----
+
+uint64_t synapse_kv_prefix_hash(const uint8_t* bytes, size_t count) {
+    uint64_t hash = 0xcbf29ce484222325ull;
+    for (size_t i = 0; bytes != nullptr && i < count; ++i) {
+        hash ^= bytes[i];
+        hash *= 0x100000001b3ull;
+    }
+    return hash;
+}
+
+namespace synapse_kv {
+namespace {
+
+// Bytes of one layer's K (or V) rows of `length` positions.
+uint64_t prefix_rows_bytes(const Dims& dims, uint32_t length) {
+    return static_cast<uint64_t>(length) * dims.kv_heads * dims.head_dim * (dims.precision == SYNAPSE_KV_F16 ? 2 : 4);
+}
+
+bool same_key(const SynapseKvPrefixKey& a, const SynapseKvPrefixKey& b) {
+    return a.model == b.model && a.tokenizer == b.tokenizer && a.rope == b.rope && a.prefix == b.prefix;
+}
+
+void raise_status(int32_t status) {
+    if (status != SYNAPSE_KV_OK) {
+        throw Failure{status, g_last_error};
+    }
+}
+
+}  // namespace
+}  // namespace synapse_kv
+
+int32_t synapse_kv_export_prefix(SynapseKvCache* cache, uint32_t slot, uint32_t length, const SynapseKvPrefixKey* key,
+                                 uint8_t* payload, uint64_t capacity, uint64_t* bytes) {
+    if (cache == nullptr || key == nullptr || bytes == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache, key or size output");
+    }
+    return guarded([&] {
+        check_slot(*cache, slot);
+        const Dims& dims = cache->dims;
+        if (length > cache->length[slot]) {
+            invalid("export of " + std::to_string(length) + " positions from a slot holding " +
+                    std::to_string(cache->length[slot]));
+        }
+        const uint64_t rows = prefix_rows_bytes(dims, length);
+        const uint64_t total = sizeof(SynapseKvPrefixHeader) + 2 * rows * dims.layers;
+        *bytes = total;
+        if (payload == nullptr) {
+            return;
+        }
+        if (capacity < total) {
+            invalid("the payload needs " + std::to_string(total) + " bytes");
+        }
+        SynapseKvPrefixHeader header{};
+        std::memcpy(header.magic, SYNAPSE_KV_PREFIX_MAGIC, 8);
+        header.version = SYNAPSE_KV_PREFIX_VERSION;
+        header.header_bytes = sizeof(SynapseKvPrefixHeader);
+        header.key = *key;
+        header.kv_precision = dims.precision;
+        header.layer_count = dims.layers;
+        header.kv_heads = dims.kv_heads;
+        header.head_dim = dims.head_dim;
+        header.length = length;
+        header.payload_bytes = 2 * rows * dims.layers;
+        uint8_t* out = payload + sizeof(SynapseKvPrefixHeader);
+        if (length > 0) {
+            set_device(*cache);
+            flush_ops(*cache);
+            DeviceBuffer<uint8_t> staging;
+            staging.ensure(2 * rows, "prefix staging");
+            for (uint32_t layer = 0; layer < dims.layers; ++layer) {
+                GatherArgs args{};
+                args.geo = geometry(*cache, layer);
+                args.slot = static_cast<int32_t>(slot);
+                args.first = 0;
+                args.count = static_cast<int32_t>(length);
+                args.keys = staging.pointer;
+                args.values = staging.pointer + rows;
+                hipError_t error = launch_gather(launch_for(*cache, SYNAPSE_KV_KERNEL_GATHER, true), args,
+                                                 dims.precision == SYNAPSE_KV_F16);
+                if (error == hipSuccess) {
+                    error = hipStreamSynchronize(cache->stream);
+                }
+                if (error == hipSuccess) {
+                    error = hipMemcpy(out + 2 * rows * layer, staging.pointer, 2 * rows, hipMemcpyDeviceToHost);
+                }
+                if (error != hipSuccess) {
+                    staging.reset();
+                    check_hip(error, "prefix export");
+                }
+            }
+            staging.reset();
+        }
+        header.checksum = synapse_kv_prefix_hash(out, header.payload_bytes);
+        std::memcpy(payload, &header, sizeof(header));
+    });
+}
+
+int32_t synapse_kv_import_prefix(SynapseKvCache* cache, uint32_t slot, const SynapseKvPrefixKey* key,
+                                 const uint8_t* payload, uint64_t bytes, uint32_t* length) {
+    if (cache == nullptr || key == nullptr || payload == nullptr || length == nullptr) {
+        return record(SYNAPSE_KV_NULL_POINTER, "null pointer: cache, key, payload or length output");
+    }
+    return guarded([&] {
+        check_slot(*cache, slot);
+        const Dims& dims = cache->dims;
+        if (bytes < sizeof(SynapseKvPrefixHeader)) {
+            invalid("a prefix payload starts with a 128-byte header");
+        }
+        SynapseKvPrefixHeader header;
+        std::memcpy(&header, payload, sizeof(header));
+        if (std::memcmp(header.magic, SYNAPSE_KV_PREFIX_MAGIC, 8) != 0 || header.version != SYNAPSE_KV_PREFIX_VERSION ||
+            header.header_bytes != sizeof(SynapseKvPrefixHeader)) {
+            invalid("not a version 1 prefix payload");
+        }
+        if (!same_key(header.key, *key)) {
+            invalid("the payload's prefix key differs from the requested one");
+        }
+        if (header.kv_precision != dims.precision || header.layer_count != dims.layers ||
+            header.kv_heads != dims.kv_heads || header.head_dim != dims.head_dim) {
+            invalid("the payload's KV type or shape differs from the cache's");
+        }
+        if (header.length > dims.max_positions) {
+            invalid("the payload holds more positions than the context");
+        }
+        const uint64_t rows = prefix_rows_bytes(dims, header.length);
+        if (header.payload_bytes != 2 * rows * dims.layers || bytes < sizeof(header) + header.payload_bytes) {
+            invalid("the payload's size does not match its header");
+        }
+        const uint8_t* rows_in = payload + sizeof(header);
+        if (synapse_kv_prefix_hash(rows_in, header.payload_bytes) != header.checksum) {
+            invalid("the payload's checksum does not match its rows");
+        }
+        if (cache->length[slot] != 0 || cache->capacity[slot] != 0) {
+            invalid("import needs an empty slot (release it first)");
+        }
+        if (header.length > 0) {
+            raise_status(synapse_kv_reserve(cache, slot, header.length));
+            set_device(*cache);
+            flush_ops(*cache);
+            DeviceBuffer<uint8_t> staging;
+            staging.ensure(2 * rows, "prefix staging");
+            for (uint32_t layer = 0; layer < dims.layers; ++layer) {
+                hipError_t error = hipStreamSynchronize(cache->stream);  // the staging's previous layer is written
+                if (error == hipSuccess) {
+                    error = hipMemcpy(staging.pointer, rows_in + 2 * rows * layer, 2 * rows, hipMemcpyHostToDevice);
+                }
+                GatherArgs args{};
+                args.geo = geometry(*cache, layer);
+                args.slot = static_cast<int32_t>(slot);
+                args.first = 0;
+                args.count = static_cast<int32_t>(header.length);
+                args.keys = staging.pointer;
+                args.values = staging.pointer + rows;
+                if (error == hipSuccess) {
+                    error = launch_scatter(launch_for(*cache, SYNAPSE_KV_KERNEL_GATHER, true), args,
+                                           dims.precision == SYNAPSE_KV_F16);
+                }
+                if (error != hipSuccess) {
+                    staging.reset();
+                    check_hip(error, "prefix import");
+                }
+            }
+            check_hip(hipStreamSynchronize(cache->stream), "prefix import");
+            staging.reset();
+            cache->length[slot] = header.length;
+            cache->fold_next[slot] = -1;
+            if (cache->activation.enabled != 0) {
+                // Key summaries of the imported blocks (the keys below the length).
+                std::vector<int32_t> blocks;
+                for (uint32_t position = 0; position < header.length; position += kStepKeys) {
+                    blocks.push_back(slot_page(*cache, slot, position / dims.page_tokens));
+                    blocks.push_back(static_cast<int32_t>((position % dims.page_tokens) / kStepKeys));
+                    blocks.push_back(static_cast<int32_t>(std::min<uint32_t>(kStepKeys, header.length - position)));
+                }
+                const size_t blob = blocks.size() * sizeof(int32_t);
+                cache->op_blob.ensure(blob, "operation buffer");
+                void* upload = cache->uploader.acquire(blob);
+                std::memcpy(upload, blocks.data(), blob);
+                cache->uploader.copy(cache->op_blob.pointer, blob, cache->stream);
+                SummaryArgs summary{};
+                summary.geo = geometry(*cache, 0);
+                summary.summaries = cache->summaries.pointer;
+                summary.summary_page_bytes = cache->summary_page_bytes;
+                summary.blocks = reinterpret_cast<const int32_t*>(cache->op_blob.pointer);
+                summary.count = static_cast<int32_t>(blocks.size() / 3);
+                summary.first_layer = 0;
+                summary.layers = static_cast<int32_t>(dims.layers);
+                check_hip(launch_summaries(launch_for(*cache, SYNAPSE_KV_KERNEL_APPEND, true), summary,
+                                           dims.precision == SYNAPSE_KV_F16),
+                          "key summaries");
+            }
+        }
+        *length = header.length;
+    });
+}
+
 int32_t synapse_kv_rope_table(uint32_t head_dim, float theta, float yarn_factor, uint32_t yarn_original,
                               uint32_t positions, float* cosines, float* sines) {
     if (cosines == nullptr || sines == nullptr) {

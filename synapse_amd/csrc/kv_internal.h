@@ -282,6 +282,7 @@ int prefill_resident_blocks(int device, int head_dim, int group);
 // Prefill items [first, first + items) with `tiles` (1 or kPrefillTiles) column tiles of 16 tokens per wave.
 hipError_t launch_prefill(const Launch& launch, const AttentionArgs& args, int first, int items, int tiles, bool fp16);
 hipError_t launch_gather(const Launch& launch, const GatherArgs& args, bool fp16);
+hipError_t launch_scatter(const Launch& launch, const GatherArgs& args, bool fp16);
 hipError_t launch_summaries(const Launch& launch, const SummaryArgs& args, bool fp16);
 // Key-bound selection (the largest job has `most_candidates` candidates), with args.summary_count summary items.
 hipError_t launch_select(const Launch& launch, const SelectArgs& args, int most_candidates, bool fp16);

@@ -314,6 +314,37 @@ class PagedKvCache:
         self.library.check(self.library.c_page_stats(self.handle, ctypes.byref(stats)))
         return {name: getattr(stats, name) for name, _ in PageStats._fields_ if name != "reserved"}
 
+    def export_prefix(self, slot: int, length: int, key) -> bytes:
+        """Positions 0..length-1 of `slot` as a persistent prefix payload keyed by `key` (a PrefixKey or a
+        (model, tokenizer, rope, prefix) tuple): synapse_kv_export_prefix."""
+        from .native import PrefixKey
+
+        key = key if isinstance(key, PrefixKey) else PrefixKey(*key)
+        size = ctypes.c_uint64()
+        self.library.check(self.library.c_export_prefix(self.handle, slot, length, ctypes.byref(key), None, 0,
+                                                        ctypes.byref(size)))
+        payload = (ctypes.c_uint8 * size.value)()
+        self.library.check(self.library.c_export_prefix(self.handle, slot, length, ctypes.byref(key), payload,
+                                                        size.value, ctypes.byref(size)))
+        return bytes(payload)
+
+    def import_prefix(self, slot: int, key, payload: bytes) -> int:
+        """Loads a payload into the empty `slot`; returns the positions it holds (synapse_kv_import_prefix)."""
+        from .native import PrefixKey
+
+        key = key if isinstance(key, PrefixKey) else PrefixKey(*key)
+        buffer = (ctypes.c_uint8 * len(payload)).from_buffer_copy(payload)
+        length = ctypes.c_uint32()
+        self.library.check(self.library.c_import_prefix(self.handle, slot, ctypes.byref(key), buffer, len(payload),
+                                                        ctypes.byref(length)))
+        return int(length.value)
+
+    def prefix_hash(self, tokens) -> int:
+        """FNV-1a 64 of the token ids as little-endian int32 (synapse_kv_prefix_hash)."""
+        data = np.ascontiguousarray(tokens, dtype="<i4").tobytes()
+        buffer = (ctypes.c_uint8 * max(1, len(data))).from_buffer_copy(data or b"\0")
+        return int(self.library.c_prefix_hash(buffer, len(data)))
+
     def read_kv(self, slot: int, layer: int, first: int, count: int) -> tuple[np.ndarray, np.ndarray]:
         """K and V of positions [first, first + count) as [count][kv_heads][head_dim] in the storage type
         (float32, or uint16 FP16 bit patterns)."""

@@ -211,8 +211,35 @@ class Profile(ctypes.Structure):
 
 
 # Sizes pinned on both sides of the ABI (include/synapse_kv.h static assertions).
+class PrefixKey(ctypes.Structure):
+    """SynapseKvPrefixKey: what a persistent prefix payload is keyed by (ADR-018-prompt-prefix-reuse.md:42-44)."""
+
+    _fields_ = [("model", ctypes.c_uint64), ("tokenizer", ctypes.c_uint64), ("rope", ctypes.c_uint64), ("prefix", ctypes.c_uint64)]
+
+
+class PrefixHeader(ctypes.Structure):
+    """SynapseKvPrefixHeader: the 128-byte header of a prefix payload."""
+
+    _fields_ = [
+        ("magic", ctypes.c_char * 8),
+        ("version", ctypes.c_uint32),
+        ("header_bytes", ctypes.c_uint32),
+        ("key", PrefixKey),
+        ("kv_precision", ctypes.c_uint32),
+        ("layer_count", ctypes.c_uint32),
+        ("kv_heads", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("length", ctypes.c_uint32),
+        ("reserved0", ctypes.c_uint32),
+        ("payload_bytes", ctypes.c_uint64),
+        ("checksum", ctypes.c_uint64),
+        ("reserved", ctypes.c_uint8 * 40),
+    ]
+
+
 STRUCT_SIZES = {DeviceInfo: 152, BatchToken: 16, CacheDesc: 64, PageStats: 40, Profile: 128, Matrix: 24,
-                Projection: 48, PageActivation: 24, LayerOffsets: 120, DecoderDesc: 136}
+                Projection: 48, PageActivation: 24, LayerOffsets: 120, DecoderDesc: 136, PrefixKey: 32,
+                PrefixHeader: 128}
 for _struct, _size in STRUCT_SIZES.items():
     assert ctypes.sizeof(_struct) == _size, (_struct.__name__, ctypes.sizeof(_struct))
 
@@ -225,6 +252,9 @@ _SIZE = ctypes.c_size_t
 # name -> (restype, argtypes); the complete exported surface of include/synapse_kv.h.
 EXPORTS = {
     "synapse_kv_abi_version": (_U32, []),
+    "synapse_kv_prefix_hash": (_U64, [_P, _SIZE]),
+    "synapse_kv_export_prefix": (_I32, [_P, _U32, _U32, ctypes.POINTER(PrefixKey), _P, _U64, ctypes.POINTER(_U64)]),
+    "synapse_kv_import_prefix": (_I32, [_P, _U32, ctypes.POINTER(PrefixKey), _P, _U64, ctypes.POINTER(_U32)]),
     "synapse_kv_probe": (_I32, [ctypes.POINTER(DeviceInfo)]),
     "synapse_kv_last_error": (_SIZE, [ctypes.c_char_p, _SIZE]),
     "synapse_kv_cache_create": (_I32, [ctypes.POINTER(CacheDesc), ctypes.POINTER(_P)]),

@@ -281,3 +281,29 @@ def test_gpu_abi_errors_follow_ffi_rs(native):
     assert native.g_decoder_reserve(None, 0, 0) == 1
     assert native.g_decoder_kv_bytes(None) == 0
     native.g_decoder_destroy(None)
+
+
+def test_prefix_hash_is_fnv1a_64(native):
+    """Published FNV-1a 64 vectors (offset basis for the empty input; "a"; "foobar"), and token ids hash as their
+    little-endian int32 bytes."""
+    def digest(data: bytes) -> int:
+        buffer = (ctypes.c_uint8 * max(1, len(data))).from_buffer_copy(data or b"\0")
+        return int(native.c_prefix_hash(buffer, len(data)))
+
+    assert digest(b"") == 0xcbf29ce484222325
+    assert digest(b"a") == 0xaf63dc4c8601ec8c
+    assert digest(b"foobar") == 0x85944171f73967e8
+    assert int(native.c_prefix_hash(None, 0)) == 0xcbf29ce484222325
+    tokens = np.array([7, 151643, 0, -1], dtype="<i4")
+    assert digest(tokens.tobytes()) != digest(tokens[:3].tobytes())
+
+
+def test_prefix_entry_points_check_pointers(native):
+    from synapse_amd.native import PrefixKey
+
+    key = PrefixKey(1, 2, 3, 4)
+    size = ctypes.c_uint64()
+    length = ctypes.c_uint32()
+    assert native.c_export_prefix(None, 0, 0, ctypes.byref(key), None, 0, ctypes.byref(size)) == 1
+    assert native.c_import_prefix(None, 0, ctypes.byref(key), None, 0, ctypes.byref(length)) == 1
+    assert "null pointer" in native.last_error()
