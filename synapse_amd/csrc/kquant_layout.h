@@ -33,6 +33,7 @@ namespace synapse_kv {
 constexpr uint32_t kEncodingQ8_0 = 8;
 constexpr uint32_t kEncodingQ4K = 12;
 constexpr uint32_t kEncodingQ6K = 14;
+constexpr uint32_t kEncodingMixedK = 0xFFu;  // a decode launch over Q4_K and Q6_K segments together
 constexpr int kSuperBlockValues = 256;
 constexpr int kQ4KBlockBytes = 144;
 constexpr int kQ6KBlockBytes = 210;

@@ -171,7 +171,7 @@ struct ProjectionSegment {
     int32_t rows;
     int32_t first_tile;
     int32_t out_column;
-    int32_t pad;
+    uint32_t encoding;  // GGML type of this segment's matrix
 };
 
 struct ProjectionArgs {
@@ -191,7 +191,8 @@ struct ProjectionArgs {
     int32_t slices;          // decode: column slices (projection_decode_slices)
     float* partials;         // decode: [slices][16][partial_stride] per-slice sums (scratch)
     int64_t partial_stride;  // total_tiles * 16
-    uint32_t encoding;       // GGML type of every segment: 8 (Q8_0), 12 (Q4_K) or 14 (Q6_K)
+    uint32_t encoding;       // GGML type of every segment: 8 (Q8_0), 12 (Q4_K) or 14 (Q6_K); decode launches also
+                             // take kEncodingMixedK: K-quant segments of both types (each segment's own field)
     int32_t pad;
     float* sums;             // prompt runs of Q4_K: [tokens][padded_columns / 8] sums of 8 inputs (scratch)
 };

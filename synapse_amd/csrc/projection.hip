@@ -484,7 +484,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
     constexpr int TW = decode_tiles_per_wave<E>();
     __shared__ bf16x8 staged[kDecodeSliceChunks * kParts * 2 * 64];
     // Q4_K: per chunk, 8-column group and token, the sum of the 8 inputs.
-    __shared__ float group_sums[E == kEncodingQ4K ? kDecodeSliceChunks * 8 * 16 : 1];
+    constexpr bool kSums = E == kEncodingQ4K || E == kEncodingMixedK;
+    __shared__ float group_sums[kSums ? kDecodeSliceChunks * 8 * 16 : 1];
     const int slice = blockIdx.y;
     const int k0 = slice * a.chunks / a.slices;
     const int k1 = (slice + 1) * a.chunks / a.slices;
@@ -516,15 +517,38 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
     // 2. This wave's codes and scales for the slice, issued after the input loads: loads complete in issue order,
     //    so the split below waits for the input only, while the weight stream stays in flight.
     //    A tile past the last loads the last tile again.
-    ChunkWeights<E> batch[TW][kDecodeSliceChunks];
+    //    A launch over both K-quant types (kEncodingMixedK) keeps Q6_K-shaped registers and branches per wave on its
+    //    tile's segment (uniform per wave); a Q4_K tile fills only the first half of each code vector.
+    constexpr uint32_t kStored = E == kEncodingMixedK ? kEncodingQ6K : E;
+    ChunkWeights<kStored> batch[TW][kDecodeSliceChunks];
+    bool q4k_tile[TW];
 #pragma unroll
     for (int k = 0; k < TW; ++k) {
         ProjectionSegment seg;
         const int tile = locate_tile(a, min(first_tile + k, a.total_tiles - 1), seg);
         const size_t first_chunk = static_cast<size_t>(tile) * a.chunks + k0;
+        q4k_tile[k] = E == kEncodingQ4K || (E == kEncodingMixedK && seg.encoding == kEncodingQ4K);
+        if constexpr (E == kEncodingMixedK) {
+            if (q4k_tile[k]) {
 #pragma unroll
-        for (int i = 0; i < kDecodeSliceChunks; ++i) {
-            batch[k][i] = load_chunk<E>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
+                for (int i = 0; i < kDecodeSliceChunks; ++i) {
+                    const ChunkWeights<kEncodingQ4K> w =
+                        load_chunk<kEncodingQ4K>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
+                    batch[k][i].codes = w.codes;
+                    batch[k][i].factor = w.factor;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kDecodeSliceChunks; ++i) {
+                    batch[k][i] = load_chunk<kEncodingQ6K>(seg.codes, seg.scales, first_chunk + min(i, count - 1),
+                                                           lane, g);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kDecodeSliceChunks; ++i) {
+                batch[k][i] = load_chunk<E>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -553,7 +577,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
         for (int p = 0; p < kParts; ++p) {
             staged[((chunk * kParts + p) * 2 + block) * 64 + 16 * lane_group + t] = parts[p];
         }
-        if constexpr (E == kEncodingQ4K) {
+        if constexpr (kSums) {
             float sum = raw[j][0][0];
 #pragma unroll
             for (int i = 1; i < 8; ++i) {
@@ -582,7 +606,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
                 }
             }
             float xsum[1][2] = {};
-            if constexpr (E == kEncodingQ4K) {
+            if constexpr (kSums) {
 #pragma unroll
                 for (int b = 0; b < 2; ++b) {
                     const float* four = group_sums + (i * 8 + 4 * b) * 16 + (lane & 15);
@@ -591,7 +615,18 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
             }
 #pragma unroll
             for (int k = 0; k < TW; ++k) {
-                multiply_chunk<E, 1>(batch[k][i], input, xsum, acc[k]);
+                if constexpr (E == kEncodingMixedK) {
+                    if (q4k_tile[k]) {
+                        ChunkWeights<kEncodingQ4K> w;
+                        w.codes = batch[k][i].codes;
+                        w.factor = batch[k][i].factor;
+                        multiply_chunk<kEncodingQ4K, 1>(w, input, xsum, acc[k]);
+                    } else {
+                        multiply_chunk<kEncodingQ6K, 1>(batch[k][i], input, xsum, acc[k]);
+                    }
+                } else {
+                    multiply_chunk<E, 1>(batch[k][i], input, xsum, acc[k]);
+                }
             }
         }
     }
@@ -666,6 +701,12 @@ hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, i
             case kEncodingQ6K:
                 SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ6K>,
                                   dim3((tiles + decode_tiles<kEncodingQ6K>() - 1) / decode_tiles<kEncodingQ6K>(), args.slices),
+                                  block, launch, args);
+                break;
+            case kEncodingMixedK:
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingMixedK>,
+                                  dim3((tiles + decode_tiles<kEncodingMixedK>() - 1) / decode_tiles<kEncodingMixedK>(),
+                                       args.slices),
                                   block, launch, args);
                 break;
             default:

@@ -164,9 +164,15 @@ DeferredSums launch_run(SynapseKvWeights& weights, const SynapseKvProjection& p,
         seg.rows = static_cast<int32_t>(m.rows);
         seg.first_tile = tiles;
         seg.out_column = static_cast<int32_t>(p.out_column[first + s]);
+        seg.encoding = m.encoding;
         tiles += q8_tiles(static_cast<int>(m.rows));
     }
-    const uint32_t encoding = weights.matrices[p.matrix[first]].encoding;
+    uint32_t encoding = weights.matrices[p.matrix[first]].encoding;
+    for (uint32_t s = 1; s < count; ++s) {
+        if (args.segment[s].encoding != encoding) {
+            encoding = kEncodingMixedK;  // a decode run over Q4_K and Q6_K segments
+        }
+    }
     args.encoding = encoding;
     args.segments = static_cast<int32_t>(count);
     args.columns = static_cast<int32_t>(columns);
@@ -253,12 +259,17 @@ void validate_projection(SynapseKvWeights& weights, const SynapseKvProjection& p
 
 void project(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output) {
     validate_projection(weights, p, input, output);
-    // Consecutive segments of one encoding share a launch (the kernels are specialised per encoding).
+    // Consecutive segments of one encoding share a launch (the kernels are specialised per encoding); decode runs
+    // (at most 16 tokens) also put Q4_K and Q6_K segments in one launch.
+    auto joins = [&](uint32_t a, uint32_t b) {
+        const uint32_t x = weights.matrices[p.matrix[a]].encoding;
+        const uint32_t y = weights.matrices[p.matrix[b]].encoding;
+        return x == y || (p.tokens <= 16 && is_kquant(x) && is_kquant(y));
+    };
     uint32_t first = 0;
     while (first < p.segments) {
         uint32_t count = 1;
-        const uint32_t encoding = weights.matrices[p.matrix[first]].encoding;
-        while (first + count < p.segments && weights.matrices[p.matrix[first + count]].encoding == encoding) {
+        while (first + count < p.segments && joins(first, first + count)) {
             ++count;
         }
         launch_run(weights, p, first, count, input, output);
@@ -274,7 +285,9 @@ DeferredSums project_deferred(SynapseKvWeights& weights, const SynapseKvProjecti
     bool single = p.tokens <= 16;
     for (uint32_t s = 0; s < p.segments; ++s) {
         const DeviceMatrix& m = weights.matrices[p.matrix[s]];
-        single = single && !m.has_bias && m.encoding == weights.matrices[p.matrix[0]].encoding;
+        const uint32_t first_encoding = weights.matrices[p.matrix[0]].encoding;
+        single = single && !m.has_bias &&
+                 (m.encoding == first_encoding || (is_kquant(m.encoding) && is_kquant(first_encoding)));
     }
     if (!single) {
         project(weights, p, input, output);
