@@ -46,6 +46,8 @@ extern "C" {
 #define SYNAPSE_KV_OPTION_DECODE_PREFETCH 4u /* 1: FP16 decode keeps the next step's loads in flight (two register sets) */
 #define SYNAPSE_KV_OPTION_PROFILE_EVERY 5u   /* profile mode times every n-th launch of each kernel kind (default 1) */
 #define SYNAPSE_KV_OPTION_SHARED_PREFIX 6u  /* 1 (default): FP16 decode reads pages shared by several step tokens once */
+#define SYNAPSE_KV_OPTION_FUSED_SUMS 7u     /* decoder on this cache: 1 (default) adds the o_proj and gate/up slice sums
+                                               inside the next RMS norm and SwiGLU; 0: separate reduces (same bits) */
 
 /* GpuDeviceInfo (native/synapse-gpu/src/Features/GpuKernels/mod.rs:20-31), 152 bytes. */
 typedef struct SynapseKvDeviceInfo {

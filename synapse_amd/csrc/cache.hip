@@ -210,6 +210,7 @@ struct SynapseKvCache {
     int32_t prefill_slots = 256;         // resident prefill workgroups on the device
     uint32_t prefetch = 1;  // decode kernel variant: 1 = two register sets, next step's loads in flight
     uint32_t shared_prefix = 1;  // 1: decode reads copy-on-write pages shared by several step tokens once
+    uint32_t fused_sums = 1;     // decoder: 1 adds deferred slice sums in the consuming kernels
     SynapseKvPageActivation activation{};  // KV page activation (enabled = 0: dense)
     synapse_kv::DeviceBuffer<uint8_t> summaries;  // per pool page: key minima and maxima of its 64-key blocks
     uint64_t summary_page_bytes = 0;
@@ -1374,6 +1375,10 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
 
 using namespace synapse_kv;
 
+namespace synapse_kv {
+bool cache_fused_sums(const SynapseKvCache& cache) { return cache.fused_sums != 0; }
+}  // namespace synapse_kv
+
 extern "C" {
 
 uint32_t synapse_kv_abi_version(void) { return SYNAPSE_KV_ABI_VERSION; }
@@ -1457,6 +1462,8 @@ int32_t synapse_kv_set_option(SynapseKvCache* cache, uint32_t option, uint32_t v
                                                         cache->dims.head_dim, cache->prefetch != 0);
         } else if (option == SYNAPSE_KV_OPTION_SHARED_PREFIX) {
             cache->shared_prefix = value != 0 ? 1 : 0;
+        } else if (option == SYNAPSE_KV_OPTION_FUSED_SUMS) {
+            cache->fused_sums = value != 0 ? 1 : 0;
         } else if (option == SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS) {
             if (value % kStepKeys != 0) {
                 invalid("prefill split keys must be 0 (automatic) or a multiple of 64");

@@ -614,8 +614,13 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
         check_status(synapse_kv_append_attention(m.cache, layer, m.qkv.pointer, qkv_width, m.attention.pointer, hidden));
         // Decode steps leave the output and gate/up projections' slice sums to the kernels that consume them: the
         // residual add runs inside the feed-forward norm and the gate/up sums inside SwiGLU (two launches fewer).
-        const DeferredSums o = project_deferred_sums(m, {{base + 3, 0}}, n, m.attention.pointer, hidden,
-                                                     m.hidden.pointer, hidden, true);
+        const bool fused = cache_fused_sums(*m.cache);
+        const DeferredSums o = fused ? project_deferred_sums(m, {{base + 3, 0}}, n, m.attention.pointer, hidden,
+                                                             m.hidden.pointer, hidden, true)
+                                     : DeferredSums{};
+        if (!fused) {
+            project(m, {{base + 3, 0}}, n, m.attention.pointer, hidden, m.hidden.pointer, hidden, true);
+        }
         if (o.deferred) {
             hipLaunchKernelGGL(residual_norm_kernel, dim3(n), dim3(256), 0, m.stream, m.hidden.pointer, o, ffn_norm,
                                hidden, d.rms_epsilon, m.normalized.pointer);
@@ -625,9 +630,14 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
                                m.normalized.pointer);
         }
         check_hip(hipGetLastError(), "feed-forward norm");
-        const DeferredSums gate_up = project_deferred_sums(m, {{base + 4, 0}, {base + 5, ffn}}, n,
-                                                           m.normalized.pointer, hidden, m.gate_up.pointer, 2 * ffn,
-                                                           false);
+        DeferredSums gate_up;
+        if (fused) {
+            gate_up = project_deferred_sums(m, {{base + 4, 0}, {base + 5, ffn}}, n, m.normalized.pointer, hidden,
+                                            m.gate_up.pointer, 2 * ffn, false);
+        } else {
+            project(m, {{base + 4, 0}, {base + 5, ffn}}, n, m.normalized.pointer, hidden, m.gate_up.pointer, 2 * ffn,
+                    false);
+        }
         if (gate_up.deferred) {
             hipLaunchKernelGGL(reduce_swiglu_kernel, dim3((ffn + 255) / 256, n), dim3(256), 0, m.stream, gate_up, ffn,
                                m.feed_forward.pointer);

@@ -323,6 +323,8 @@ struct DeferredSums {
 struct SynapseKvWeights;
 
 namespace synapse_kv {
+// SYNAPSE_KV_OPTION_FUSED_SUMS of a cache (the decoder built on it reads it per step).
+bool cache_fused_sums(const SynapseKvCache& cache);
 DeferredSums project_deferred(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input,
                               float* output);
 }  // namespace synapse_kv

@@ -36,6 +36,7 @@ OPTION_PREFILL_SPLIT_KEYS = 3
 OPTION_DECODE_PREFETCH = 4
 OPTION_PROFILE_EVERY = 5
 OPTION_SHARED_PREFIX = 6
+OPTION_FUSED_SUMS = 7
 
 SELECT_KEY_BOUND = 0
 SELECT_RANDOM = 1

@@ -152,3 +152,26 @@ def test_decoder_through_the_libsynapse_gpu_abi(torch_gpu):
     assert library.g_decoder_kv_bytes(gpu_abi.handle) > native_abi.kv_bytes
     native_abi.close()
     gpu_abi.close()
+
+
+@pytest.mark.parametrize("encodings", [None, "q4_k_m"])
+def test_fused_slice_sums_are_bit_identical_to_separate_reduces(torch_gpu, encodings):
+    """Decode steps add the o_proj and gate/up slice sums inside the feed-forward norm and SwiGLU kernels; with
+    SYNAPSE_KV_OPTION_FUSED_SUMS = 0 they run as separate reduce launches. The additions are the same and in the
+    same order, so the logits are bit-identical (prompt steps of more than 16 tokens take the unfused path in
+    both)."""
+    from synapse_amd.decoder import q4_k_m
+    from synapse_amd.native import OPTION_FUSED_SUMS
+
+    say("decoder fused sums", encodings)
+    shape = DecoderShape(layers=2, hidden=512, feed_forward=1024, heads=8, kv_heads=2, head_dim=64, vocabulary=300,
+                         context=512, session_slots=3, step_tokens=128, logits_rows=8, growth=256, kv_precision="f16")
+    blob, layout = synthetic_model(shape, seed=13, encodings=q4_k_m if encodings else None)
+    fused = Decoder(blob, layout, shape)
+    separate = Decoder(blob, layout, shape)
+    separate.set_option(OPTION_FUSED_SUMS, 0)
+    rng = np.random.default_rng(13)
+    for tokens in steps(rng, shape):
+        assert np.array_equal(fused.forward(tokens).view(np.uint32), separate.forward(tokens).view(np.uint32))
+    fused.close()
+    separate.close()
