@@ -240,7 +240,7 @@ int32_t synapse_kv_page_stats(SynapseKvCache* cache, SynapseKvPageStats* stats);
 int32_t synapse_kv_read_kv(SynapseKvCache* cache, uint32_t slot, uint32_t layer, uint32_t first, uint32_t count,
                            void* keys, void* values);
 
-/* ---- Persistent prefix payloads (ADR-018's next step) ----
+/* ---- Persistent prefix payloads (the persistent prefix cache planned as ADR-018's next step) ----
  * A slot's first `length` positions serialized for a prefix cache outside the process: payloads keyed by model,
  * tokenizer, RoPE, KV type and prefix hash (ADR-018-prompt-prefix-reuse.md:42-44). The library writes and checks
  * the payload; where it is stored (the reference plans ZoneTree metadata and files on disk) is the caller's.
