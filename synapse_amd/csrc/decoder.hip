@@ -73,20 +73,21 @@ __global__ __launch_bounds__(256) void embed_kquant_kernel(const uint8_t* table,
 // synapse_rms_norm (elementwise.cu:17-52): y = x * (1 / sqrt(mean(x^2) + eps)) * w, one workgroup per row; with
 // `gather` row r reads input row gather[r] (the logits rows). Each thread keeps its columns (16-byte groups, up to
 // kNormGroups of them, i.e. hidden <= 8,192) in registers: all loads are issued before the sum, and the row is read
-// once. The sum of squares is reduced per wave, then across the workgroup's waves in order.
-constexpr int kNormGroups = 8;
+// once. The sum of squares is reduced per wave, then across the workgroup's 16 waves in order.
+constexpr int kNormThreads = 1024;  // one workgroup of 16 waves per row: more loads in flight per row
+constexpr int kNormGroups = 2;
 #pragma clang fp contract(off)
-// y = x * (1 / sqrt(mean(x^2) + eps)) * w for one row held by the workgroup (256 threads), columns 4 j' apart:
-// thread i holds float4 groups i + 256 j (zeros past the row).
+// y = x * (1 / sqrt(mean(x^2) + eps)) * w for one row held by the workgroup (kNormThreads threads):
+// thread i holds float4 groups i + kNormThreads j (zeros past the row).
 __device__ inline void normalize_row(const float4 (&values)[kNormGroups], const float* weight, uint32_t columns,
                                      float epsilon, float* y_row) {
-    __shared__ float partial[4];
+    __shared__ float partial[kNormThreads / 64];
     const float4* w = reinterpret_cast<const float4*>(weight);
     const uint32_t groups = columns / 4;
     float4 scales[kNormGroups];
 #pragma unroll
     for (int j = 0; j < kNormGroups; ++j) {
-        const uint32_t index = threadIdx.x + 256 * j;
+        const uint32_t index = threadIdx.x + kNormThreads * j;
         scales[j] = index < groups ? w[index] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     float sum = 0.0f;
@@ -105,12 +106,16 @@ __device__ inline void normalize_row(const float4 (&values)[kNormGroups], const 
         partial[threadIdx.x >> 6] = sum;
     }
     __syncthreads();
-    const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    float total = partial[0];
+#pragma unroll
+    for (int wave = 1; wave < kNormThreads / 64; ++wave) {
+        total += partial[wave];
+    }
     const float scale = 1.0f / sqrtf(total / static_cast<float>(columns) + epsilon);
     float4* y = reinterpret_cast<float4*>(y_row);
 #pragma unroll
     for (int j = 0; j < kNormGroups; ++j) {
-        const uint32_t index = threadIdx.x + 256 * j;
+        const uint32_t index = threadIdx.x + kNormThreads * j;
         if (index < groups) {
             const float4 v = values[j];
             const float4 c = scales[j];
@@ -119,8 +124,9 @@ __device__ inline void normalize_row(const float4 (&values)[kNormGroups], const 
     }
 }
 
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float* input, const int32_t* gather, const float* weight,
-                                                       uint32_t columns, float epsilon, float* output) {
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* input, const int32_t* gather,
+                                                                const float* weight, uint32_t columns, float epsilon,
+                                                                float* output) {
     const int row = blockIdx.x;
     const size_t source = gather != nullptr ? static_cast<size_t>(gather[row]) : static_cast<size_t>(row);
     const float4* x = reinterpret_cast<const float4*>(input + source * columns);
@@ -128,7 +134,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* input, const
     float4 values[kNormGroups];
 #pragma unroll
     for (int j = 0; j < kNormGroups; ++j) {
-        const uint32_t index = threadIdx.x + 256 * j;
+        const uint32_t index = threadIdx.x + kNormThreads * j;
         values[j] = index < groups ? x[index] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     normalize_row(values, weight, columns, epsilon, output + static_cast<size_t>(row) * columns);
@@ -163,15 +169,16 @@ __device__ inline float4 slice_sum4(const DeferredSums& d, size_t offset) {
 // The output projection's reduce fused with the next RMS norm (one launch instead of two): hidden[t] += the
 // projection's slice sums (reduce_kernel with accumulate, in the same order), written back, then normalized into
 // `output` as rms_norm_kernel does. One workgroup per token.
-__global__ __launch_bounds__(256) void residual_norm_kernel(float* hidden, DeferredSums o, const float* weight,
-                                                            uint32_t columns, float epsilon, float* output) {
+__global__ __launch_bounds__(kNormThreads) void residual_norm_kernel(float* hidden, DeferredSums o,
+                                                                     const float* weight, uint32_t columns,
+                                                                     float epsilon, float* output) {
     const int token = blockIdx.x;
     float4* x = reinterpret_cast<float4*>(hidden + static_cast<size_t>(token) * columns);
     const uint32_t groups = columns / 4;
     float4 values[kNormGroups];
 #pragma unroll
     for (int j = 0; j < kNormGroups; ++j) {
-        const uint32_t index = threadIdx.x + 256 * j;
+        const uint32_t index = threadIdx.x + kNormThreads * j;
         values[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (index < groups) {
             const float4 h = x[index];
@@ -355,9 +362,9 @@ void validate(const SynapseKvDecoderDesc& d) {
     if (d.hidden % 32 != 0 || d.feed_forward % 32 != 0) {
         invalid("hidden and feed-forward widths must be multiples of 32");
     }
-    if (d.hidden > 4 * 256 * kNormGroups) {
+    if (d.hidden > 4 * kNormThreads * kNormGroups) {
         fail(SYNAPSE_KV_UNAVAILABLE, "the RMS norm kernel keeps a row in registers: hidden widths up to " +
-                                         std::to_string(4 * 256 * kNormGroups) + " (the model has " +
+                                         std::to_string(4 * kNormThreads * kNormGroups) + " (the model has " +
                                          std::to_string(d.hidden) + ")");
     }
     if (d.kv_precision != SYNAPSE_KV_F32 && d.kv_precision != SYNAPSE_KV_F16) {
@@ -605,7 +612,7 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
         const uint32_t base = layer * kMatrices;
         const float* attention_norm = m.norms.pointer + static_cast<size_t>(2 * layer) * hidden;
         const float* ffn_norm = attention_norm + hidden;
-        hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(256), 0, m.stream, m.hidden.pointer,
+        hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(kNormThreads), 0, m.stream, m.hidden.pointer,
                            static_cast<const int32_t*>(nullptr), attention_norm, hidden, d.rms_epsilon,
                            m.normalized.pointer);
         check_hip(hipGetLastError(), "attention norm");
@@ -622,10 +629,10 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
             project(m, {{base + 3, 0}}, n, m.attention.pointer, hidden, m.hidden.pointer, hidden, true);
         }
         if (o.deferred) {
-            hipLaunchKernelGGL(residual_norm_kernel, dim3(n), dim3(256), 0, m.stream, m.hidden.pointer, o, ffn_norm,
-                               hidden, d.rms_epsilon, m.normalized.pointer);
+            hipLaunchKernelGGL(residual_norm_kernel, dim3(n), dim3(kNormThreads), 0, m.stream, m.hidden.pointer, o,
+                               ffn_norm, hidden, d.rms_epsilon, m.normalized.pointer);
         } else {
-            hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(256), 0, m.stream, m.hidden.pointer,
+            hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(kNormThreads), 0, m.stream, m.hidden.pointer,
                                static_cast<const int32_t*>(nullptr), ffn_norm, hidden, d.rms_epsilon,
                                m.normalized.pointer);
         }
@@ -652,7 +659,7 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
     }
     if (rows > 0) {
         const float* output_norm = m.norms.pointer + static_cast<size_t>(2 * d.layer_count) * hidden;
-        hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, m.stream, m.hidden.pointer,
+        hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(kNormThreads), 0, m.stream, m.hidden.pointer,
                            static_cast<const int32_t*>(m.indices.pointer + d.step_tokens), output_norm, hidden,
                            d.rms_epsilon, m.logits_input.pointer);
         check_hip(hipGetLastError(), "output norm");
