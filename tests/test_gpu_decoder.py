@@ -35,6 +35,10 @@ SHAPES = [
     ("d128 f32 no-bias", DecoderShape(layers=3, hidden=512, feed_forward=1024, heads=4, kv_heads=4, head_dim=128,
                                       vocabulary=300, context=512, session_slots=3, step_tokens=128, logits_rows=8,
                                       growth=256)),
+    # hidden 4,608: the norm kernels' 1,024 threads hold a second, partly filled float4 group of the row.
+    ("wide f16", DecoderShape(layers=1, hidden=4608, feed_forward=1024, heads=36, kv_heads=6, head_dim=128,
+                              vocabulary=256, context=512, session_slots=3, step_tokens=128, logits_rows=8,
+                              growth=256, kv_precision="f16")),
 ]
 
 
@@ -154,8 +158,8 @@ def test_decoder_through_the_libsynapse_gpu_abi(torch_gpu):
     gpu_abi.close()
 
 
-@pytest.mark.parametrize("encodings", [None, "q4_k_m"])
-def test_fused_slice_sums_are_bit_identical_to_separate_reduces(torch_gpu, encodings):
+@pytest.mark.parametrize("encodings,hidden", [(None, 512), ("q4_k_m", 512), (None, 4608)])
+def test_fused_slice_sums_are_bit_identical_to_separate_reduces(torch_gpu, encodings, hidden):
     """Decode steps add the o_proj and gate/up slice sums inside the feed-forward norm and SwiGLU kernels; with
     SYNAPSE_KV_OPTION_FUSED_SUMS = 0 they run as separate reduce launches. The additions are the same and in the
     same order, so the logits are bit-identical (prompt steps of more than 16 tokens take the unfused path in
@@ -163,9 +167,10 @@ def test_fused_slice_sums_are_bit_identical_to_separate_reduces(torch_gpu, encod
     from synapse_amd.decoder import q4_k_m
     from synapse_amd.native import OPTION_FUSED_SUMS
 
-    say("decoder fused sums", encodings)
-    shape = DecoderShape(layers=2, hidden=512, feed_forward=1024, heads=8, kv_heads=2, head_dim=64, vocabulary=300,
-                         context=512, session_slots=3, step_tokens=128, logits_rows=8, growth=256, kv_precision="f16")
+    say("decoder fused sums", encodings, hidden)
+    shape = DecoderShape(layers=2, hidden=hidden, feed_forward=1024, heads=hidden // 64,
+                         kv_heads=2 if hidden == 512 else 9, head_dim=64, vocabulary=300, context=512,
+                         session_slots=3, step_tokens=128, logits_rows=8, growth=256, kv_precision="f16")
     blob, layout = synthetic_model(shape, seed=13, encodings=q4_k_m if encodings else None)
     fused = Decoder(blob, layout, shape)
     separate = Decoder(blob, layout, shape)
