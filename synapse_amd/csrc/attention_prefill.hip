@@ -26,10 +26,9 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 
 constexpr float kNegativeInfinity = -__builtin_inff();
-// Offsets trail the running maximum by less than this (log2 units), so FP16 probabilities stay below 256.
+// Offsets trail the running maximum by less than this (log2 units), so probabilities stay below 256.
 constexpr float kLazyRescale = 8.0f;
 
 __device__ inline float fast_exp2(float value) { return __builtin_amdgcn_exp2f(value); }
@@ -285,8 +284,9 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
     };
 
     // Softmax half of a step: scores of block `step` are in `current`; it leaves block step+1's in `upcoming` and
-    // the step's FP16 probabilities in `probability`.
+    // the step's probabilities as exact FP16 pairs: p = probability + probability_lo to about FP32 accuracy.
     half8 probability[NT][2];
+    half8 probability_lo[NT][2];
     auto softmax_phase = [&](int step, auto masked_tag, floatx4(&current)[NT][4], floatx4(&upcoming)[NT][4]) __attribute__((always_inline)) {
         constexpr bool kMasked = decltype(masked_tag)::value;
         const int key0 = item.key_begin + step * kStepKeys;
@@ -353,21 +353,22 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
         }
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
+            // p < 2^kLazyRescale, so the high part is finite. The FP32 probabilities' sum is the row total: numerator
+            // and denominator carry the same weights (hi + lo = p to about 2^-22 relative).
+            float sums[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
+                float p[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    probability[c][t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(fast_exp2(current[c][t][i]));
+                    p[i] = fast_exp2(current[c][t][i]);
+                    const _Float16 high = static_cast<_Float16>(p[i]);
+                    probability[c][t >> 1][4 * (t & 1) + i] = high;
+                    probability_lo[c][t >> 1][4 * (t & 1) + i] = static_cast<_Float16>(p[i] - static_cast<float>(high));
                 }
+                sums[t] = (p[0] + p[1]) + (p[2] + p[3]);
             }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    total[c] = __builtin_amdgcn_fdot2(half2{probability[c][h][e], probability[c][h][e + 1]},
-                                                      half2{1.0f16, 1.0f16}, total[c], false);
-                }
-            }
+            total[c] += (sums[0] + sums[1]) + (sums[2] + sums[3]);
         }
         __builtin_amdgcn_s_setprio(0);
     };
@@ -383,6 +384,11 @@ __global__ __launch_bounds__(WAVES * 64) void prefill_f16_kernel(AttentionArgs a
             }
 #pragma unroll
             for (int c = 0; c < NT; ++c) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    out[c][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(value_fragment[h], probability_lo[c][h],
+                                                                        out[c][mt], 0, 0, 0);
+                }
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     out[c][mt] =
