@@ -177,8 +177,8 @@ int32_t synapse_kv_step(SynapseKvCache* cache, const SynapseKvBatchToken* tokens
 int32_t synapse_kv_step_prompt(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count,
                                size_t prompt_start);
 
-/* synapse_kv_step_prompt for callers that cannot allocate (HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). No counterpart in the reference. The step's table operations, attention plan and attention
+/* synapse_kv_step_prompt for callers that cannot allocate (tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. The step's table operations, attention plan and attention
  * partial rows go to a static device array of SYNAPSE_KV_STATIC_SCRATCH_BYTES per GPU (held until the process
  * ends) instead of buffers the cache grows; the call makes no device or pinned-host allocation (its host planning
  * uses ordinary heap memory, as every step does) and uploads from pageable memory. The layer calls of the step
@@ -186,7 +186,8 @@ int32_t synapse_kv_step_prompt(SynapseKvCache* cache, const SynapseKvBatchToken*
  * fails with INVALID_ARGUMENT and changes nothing; KV page activation is UNAVAILABLE here. Every cache on a GPU
  * shares that GPU's array, which keeps the last step's contents: from one cache's static step to the last layer
  * call of that step, no other static step may run on the same GPU (the two would race); calls of one cache on one
- * stream are ordered as usual. */
+ * stream are ordered as usual. The call itself is not capturable into a HIP graph: it waits on host events for its
+ * staging buffers and builds the plan on the host from the cache's state at call time. */
 #define SYNAPSE_KV_STATIC_SCRATCH_BYTES (64u * 1024u * 1024u)
 int32_t synapse_kv_step_static(SynapseKvCache* cache, const SynapseKvBatchToken* tokens, size_t count,
                                size_t prompt_start);

@@ -49,6 +49,9 @@ hipError_t launch_upload(const void* source, void* target, size_t bytes, hipStre
     if (bytes == 0) {
         return hipSuccess;
     }
+    if (((reinterpret_cast<uintptr_t>(source) | reinterpret_cast<uintptr_t>(target)) & 15) != 0) {
+        return hipErrorInvalidValue;  // the kernel moves 16-byte vectors
+    }
     const size_t vectors = (bytes + 15) / 16;
     const unsigned blocks = static_cast<unsigned>(std::min<size_t>((vectors + 255) / 256, 1024));
     hipLaunchKernelGGL(upload_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<const uint8_t*>(source),
@@ -149,9 +152,18 @@ struct Uploader {
         return host[index];
     }
 
+    // The copy kernel beats hipMemcpyAsync up to about 1 MiB (5.9 against 13.5 us at 64 KiB, 28.6 against 31.4 us
+    // at 1 MiB); from 4 MiB on the DMA copy is 5-15 % faster, so large one-off uploads (a page-activation summary
+    // rebuild over many pages) take it.
+    static constexpr size_t kDmaBytes = 2u << 20;
+
     void copy(void* device, size_t bytes, hipStream_t stream) {
         const int index = next;
-        check_hip(launch_upload(device_view[index], device, bytes, stream), "upload");
+        if (bytes >= kDmaBytes) {
+            check_hip(hipMemcpyAsync(device, host[index], bytes, hipMemcpyHostToDevice, stream), "upload");
+        } else {
+            check_hip(launch_upload(device_view[index], device, bytes, stream), "upload");
+        }
         check_hip(hipEventRecord(done[index], stream), "upload record");
         next ^= 1;
     }

@@ -274,7 +274,8 @@ struct Launch {
 
 // Launchers (each enqueues at most one kernel and returns the launch status).
 // Copies `bytes` from coherent pinned host memory, addressed through its device view, to device memory on `stream`
-// (a copy kernel, in place of hipMemcpyAsync for per-step uploads).
+// (a copy kernel, in place of hipMemcpyAsync for per-step uploads). Both addresses must be 16-byte aligned (the
+// kernel moves 16-byte vectors); otherwise nothing is launched and the result is hipErrorInvalidValue.
 hipError_t launch_upload(const void* source, void* target, size_t bytes, hipStream_t stream);
 hipError_t launch_table(const Launch& launch, const TableArgs& args);
 hipError_t launch_zero_pages(const Launch& launch, const PageArgs& args);

@@ -542,7 +542,9 @@ __global__ __launch_bounds__(kGemmWaves * 64, E == kEncodingQ6K ? 3 : 2) void pr
     // then the one or two chunks left.
     // The tail issues nothing (its chunk + 2 is past the end; the compiler drops loads whose values are never used,
     // so kOps would no longer count the newest operations): its first chunk waits for all but the next chunk's
-    // kOps operations, issued by the last full step or the prologue, its second chunk for everything.
+    // kOps operations, issued by the last full step or the prologue, its second chunk for everything. That count
+    // holds only while the step issues set `later`'s loads beside its copies (kOps includes them); the first-call
+    // tests on fresh weights cover tails of zero, one and two chunks for Q8_0 and K-quant matrices.
     int chunk = 0;
     for (; chunk + 3 <= chunks; chunk += 3) {
         step(chunk, set0, set2);

@@ -195,3 +195,32 @@ def test_weights_read_back_bit_exact_and_errors(torch_gpu):
     with pytest.raises(InvalidOperationError, match="device memory"):
         weights.project([(0, 0)], np.zeros((2, 96), dtype=np.float32).ctypes.data, out, tokens=2, in_stride=96)
     weights.close()
+
+
+@pytest.mark.parametrize("columns", [192, 256, 320])
+def test_prompt_first_call_on_fresh_weights(torch_gpu, columns):
+    """The first prompt run on newly created Q8_0 weights (cold memory: slow loads), for column counts of 3, 4 and 5
+    64-column chunks, so that the GEMM's three-chunk ring ends on a full round, one chunk or two: its first tail
+    chunk waits only for the copies the last full step (or the prologue) issued. The first call must equal the next
+    bit for bit, on several fresh objects, and the restatement's product."""
+    torch = torch_gpu
+    say("q8 first call", columns)
+    shapes = [(512, columns), (128, columns), (128, columns)]
+    tokens = 57
+    rng = np.random.default_rng(columns)
+    blob, matrices, blocks, biases = build_blob(rng, shapes, [True, False, True])
+    segments = [(0, 0), (1, 512), (2, 640)]
+    x = rng.standard_normal((tokens, columns)).astype(np.float32)
+    device_x = torch.from_numpy(x).cuda()
+    for trial in range(6):
+        weights = Q8Weights(blob, matrices)
+        first = torch.zeros((tokens, 768), device="cuda")
+        second = torch.zeros((tokens, 768), device="cuda")
+        weights.project(segments, device_x, first)
+        weights.project(segments, device_x, second)
+        torch.cuda.synchronize()
+        assert torch.equal(first.view(torch.int32), second.view(torch.int32)), trial
+        weights.close()
+    weights = Q8Weights(blob, matrices)
+    check(torch, weights, blocks, biases, segments, x, 768, accumulate=False)
+    weights.close()
