@@ -181,27 +181,48 @@ def prefill(cache, torch, lengths, rows: Rows, chunk=4096):
 
 
 def parse_kv_pages(text: str | None) -> dict | None:
-    """--kv-pages <budget>:<window>[:random[:seed]] (the reference CLI's option, ADR-016)."""
+    """--kv-pages <budget>:<window>[:p16|p32|p64][:random[:seed]] (the reference CLI's option, ADR-016;
+    GenerationOptions.cs:31)."""
     if text is None:
         return None
+    usage = "--kv-pages takes <budget>:<window>[:p16|p32|p64][:random[:seed]]"
     parts = text.split(":")
-    if len(parts) < 2 or len(parts) > 4 or (len(parts) > 2 and parts[2] != "random"):
-        sys.exit("--kv-pages takes <budget>:<window>[:random[:seed]]")
+    if len(parts) < 2:
+        sys.exit(usage)
     budget, window = int(parts[0]), int(parts[1])
-    random = len(parts) > 2
-    seed = int(parts[3]) if len(parts) > 3 else 0
-    name = f"kvpages{budget}w{window}" + ("r" if random else "")
-    return {"budget": budget, "window": window, "selection": "random" if random else "key_bound", "seed": seed,
-            "name": name}
+    rest = parts[2:]
+    page = 64
+    if rest and rest[0] in ("p16", "p32", "p64"):
+        page = int(rest[0][1:])
+        rest = rest[1:]
+    if len(rest) > 2 or (rest and rest[0] != "random"):
+        sys.exit(usage)
+    random = bool(rest)
+    seed = int(rest[1]) if len(rest) > 1 else 0
+    name = f"kvpages{budget}w{window}" + ("" if page == 64 else f"p{page}") + ("r" if random else "")
+    return {"budget": budget, "window": window, "page": page, "selection": "random" if random else "key_bound",
+            "seed": seed, "name": name}
 
 
 def attended_keys(position: int, activation: dict) -> int:
-    """Positions a decode token at `position` attends (KvPageSelector.Select with 64-position pages)."""
+    """Positions a decode token at `position` attends (KvPageSelector.Select)."""
+    size = activation["page"]
     count = position + 1
-    window_page = max(0, count - activation["window"]) // 64
+    window_page = max(0, count - activation["window"]) // size
     if max(0, window_page - 1) <= activation["budget"]:
         return count
-    return 64 + activation["budget"] * 64 + (count - window_page * 64)
+    return size + activation["budget"] * size + (count - window_page * size)
+
+
+def read_keys(position: int, activation: dict) -> int:
+    """Keys the decode kernel reads for that token: one 64-key block per listed page (its keys outside the page
+    masked), or the dense row."""
+    size = activation["page"]
+    count = position + 1
+    window_page = max(0, count - activation["window"]) // size
+    if max(0, window_page - 1) <= activation["budget"]:
+        return count
+    return 64 * (1 + activation["budget"] + position // size - window_page + 1)
 
 
 def cpu_baseline(torch, lengths, rows: Rows, decode_rows, threads: int) -> dict:
@@ -1003,8 +1024,8 @@ def main() -> None:
     prefill(cache, torch, lengths, rows)
     log(f"prefill {time.perf_counter() - started:.1f} s; KV bytes {cache.allocated_bytes / 2**30:.2f} GiB")
     if activation is not None:
-        cache.set_page_activation(activation["budget"], activation["window"], selection=activation["selection"],
-                                  seed=activation["seed"])
+        cache.set_page_activation(activation["budget"], activation["window"], page_tokens=activation["page"],
+                                  selection=activation["selection"], seed=activation["seed"])
 
     qkv = rows.decode(LAYERS, SEQUENCES)
     out = torch.empty((LAYERS, SEQUENCES, HEADS * HEAD_DIM), device="cuda")
@@ -1078,6 +1099,9 @@ def main() -> None:
         **({} if activation is None else {"kv_pages": {
             **activation, "attended_keys_per_step": int(statistics.mean(keys_per_step)),
             "dense_keys_per_step": int(statistics.mean(dense_keys_per_step)),
+            "read_keys_per_step": int(statistics.mean(
+                sum(read_keys(int(n) + args.warmup + index, activation) for n in lengths)
+                for index in range(args.steps))),
             "page_select_us_per_layer": round(kernels["page_select"][1] * 1e3 / kernels["page_select"][0], 2)
             if "page_select" in kernels else None}}),
         **step_statistics(per_step),

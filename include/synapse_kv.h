@@ -198,15 +198,16 @@ int32_t synapse_kv_step_static(SynapseKvCache* cache, const SynapseKvBatchToken*
  * budget_pages more pages: those with the highest bound max over the group's query heads of
  * sum_d max(q_d * min_d, q_d * max_d) over the page's per-channel key minimum and maximum (KEY_BOUND), or a seeded
  * random draw (RANDOM, the control; seed per (layer, KV head, position) as Qwen2KvPageMasks). Unselected pages
- * contribute nothing to that step's softmax. An approximation: off (enabled = 0) by default. Enabling builds the
- * per-page key summaries of everything already cached; later appends keep them current. */
+ * contribute nothing to that step's softmax. An approximation: off (enabled = 0) by default. Enabling (or changing
+ * page_tokens while enabled) builds the per-page key summaries of everything already cached; later appends keep them
+ * current. Key-bound selection ranks at most 8,192 candidate pages per row (UNAVAILABLE beyond). */
 #define SYNAPSE_KV_SELECT_KEY_BOUND 0u
 #define SYNAPSE_KV_SELECT_RANDOM 1u
 typedef struct SynapseKvPageActivation {
     uint32_t enabled;       /* 0: dense attention (default) */
     uint32_t budget_pages;  /* BudgetPages */
     uint32_t window_tokens; /* WindowTokens */
-    uint32_t page_tokens;   /* PageTokens: 64 here (16 and 32 are UNAVAILABLE) */
+    uint32_t page_tokens;   /* PageTokens: 16, 32 or 64 positions per activation page */
     uint32_t selection;     /* SYNAPSE_KV_SELECT_* */
     int32_t seed;           /* Seed of the random control */
 } SynapseKvPageActivation;

@@ -72,11 +72,11 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
             keys[key_offset<T>(d, within, i)] = stored_first;
             keys[key_offset<T>(d, within, i + half)] = stored_second;
             if (a.extend != nullptr && a.extend[index] != 0) {
-                // The block's summary covers its keys below this position: fold the new key in (MathF.Min /
-                // MathF.Max of KvPageSelector.PageBound), or start from it at the block's first position.
+                // The activation page's summary covers its keys below this position: fold the new key in
+                // (MathF.Min / MathF.Max of KvPageSelector.PageBound), or start from it at the page's first position.
                 T* summary = reinterpret_cast<T*>(a.summaries + static_cast<uint64_t>(page) * a.summary_page_bytes);
-                const int block = within / kBlockKeys;
-                const bool fresh = within % kBlockKeys == 0;
+                const int block = within / g.summary_keys;
+                const bool fresh = within % g.summary_keys == 0;
                 const int channels[2] = {i, i + half};
                 const float values[2] = {widen(stored_first), widen(stored_second)};
 #pragma unroll

@@ -211,7 +211,7 @@ __device__ inline void fetch_f16(const Geometry& geo, const int32_t* table, size
 // 2^-22 relative, or 2^-25 absolute).
 template <int D>
 __device__ inline void step_f16(const Fragments16<D>& fragments, const half8 (&query)[D / 32], WaveState<D>& state,
-                                int key0, int key_end, float scale_log2) {
+                                int key0, int key_low, int key_end, float scale_log2) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;
     const bool low_part = (lane & 8) != 0;
@@ -228,8 +228,10 @@ __device__ inline void step_f16(const Fragments16<D>& fragments, const half8 (&q
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            // key_low <= key < key_end, as one unsigned compare.
             const int key = key0 + 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
-            scores[t][i] = key < key_end ? add_half_row(scores[t][i]) * scale_log2 : kNegativeInfinity;
+            const bool visible = static_cast<uint32_t>(key - key_low) < static_cast<uint32_t>(key_end - key_low);
+            scores[t][i] = visible ? add_half_row(scores[t][i]) * scale_log2 : kNegativeInfinity;
         }
     }
     const float alpha = softmax_step(scores, state.maximum, state.sum);
@@ -258,8 +260,9 @@ __device__ inline void step_f16(const Fragments16<D>& fragments, const half8 (&q
 }
 
 // Steps [step_begin, step_end) of one KV head through the block table `table` against one column tile of queries,
-// FP16 pages: step s covers the 64 keys of block `list[s]` (KV page activation) or of block s (list null); keys at
-// or past `key_limit` are masked. The list is read with uniform (scalar) loads. With PREFETCH the next step's
+// FP16 pages: step s covers the 64-key block of keys 64 s .. (list null), or under KV page activation the activation
+// page of a.geo.summary_keys keys from key list[s] (the 64-key block holding it is read, its other keys masked); keys
+// at or past `key_limit` are masked. The list is read with uniform (scalar) loads. With PREFETCH the next step's
 // fragments are loaded before the current step is computed.
 template <int D, bool PREFETCH>
 __device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, int kv_head, int step_begin,
@@ -268,15 +271,22 @@ __device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, 
     const Geometry& geo = a.geo;
     const size_t key_region = region_offset(geo, 0, kv_head);
     const size_t value_region = region_offset(geo, 1, kv_head);
+    // A step's entry: its first visible key (a page's first key under activation, else the block's first key).
     auto first_key = [&](int step) __attribute__((always_inline)) {
-        return (list != nullptr ? load_uniform(list + step) : step) * kStepKeys;
+        return list != nullptr ? load_uniform(list + step) : step * kStepKeys;
+    };
+    const int span = geo.summary_keys;
+    auto attend = [&](const Fragments16<D>& fragments, int entry) __attribute__((always_inline)) {
+        const int low = list != nullptr ? entry : 0;
+        const int end = list != nullptr ? min(entry + span, key_limit) : key_limit;
+        step_f16<D>(fragments, query, state, entry & ~(kStepKeys - 1), low, end, a.scale_log2);
     };
     if constexpr (!PREFETCH) {
         for (int step = step_begin; step < step_end; ++step) {
             Fragments16<D> fragments;
             const int key0 = first_key(step);
-            fetch_f16<D>(geo, table, key_region, value_region, key0, fragments);
-            step_f16<D>(fragments, query, state, key0, key_limit, a.scale_log2);
+            fetch_f16<D>(geo, table, key_region, value_region, key0 & ~(kStepKeys - 1), fragments);
+            attend(fragments, key0);
         }
     } else {
         // Two register sets: the loads of the next step are in flight while the current step computes. The loop
@@ -285,26 +295,27 @@ __device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, 
         // join, and the step after it would wait for the prefetched block too); the last one or two steps follow.
         Fragments16<D> even;
         Fragments16<D> odd;
+        constexpr int kBlock = ~(kStepKeys - 1);
         int step = step_begin;
         int key0 = first_key(step);
-        fetch_f16<D>(geo, table, key_region, value_region, key0, even);
+        fetch_f16<D>(geo, table, key_region, value_region, key0 & kBlock, even);
         while (step + 2 < step_end) {
             const int key1 = first_key(step + 1);
             const int key2 = first_key(step + 2);
-            fetch_f16<D>(geo, table, key_region, value_region, key1, odd);
-            step_f16<D>(even, query, state, key0, key_limit, a.scale_log2);
-            fetch_f16<D>(geo, table, key_region, value_region, key2, even);
-            step_f16<D>(odd, query, state, key1, key_limit, a.scale_log2);
+            fetch_f16<D>(geo, table, key_region, value_region, key1 & kBlock, odd);
+            attend(even, key0);
+            fetch_f16<D>(geo, table, key_region, value_region, key2 & kBlock, even);
+            attend(odd, key1);
             step += 2;
             key0 = key2;
         }
         if (step + 1 < step_end) {
             const int key1 = first_key(step + 1);
-            fetch_f16<D>(geo, table, key_region, value_region, key1, odd);
-            step_f16<D>(even, query, state, key0, key_limit, a.scale_log2);
-            step_f16<D>(odd, query, state, key1, key_limit, a.scale_log2);
+            fetch_f16<D>(geo, table, key_region, value_region, key1 & kBlock, odd);
+            attend(even, key0);
+            attend(odd, key1);
         } else {
-            step_f16<D>(even, query, state, key0, key_limit, a.scale_log2);
+            attend(even, key0);
         }
     }
 }
@@ -367,13 +378,17 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
     const size_t key_region = region_offset(geo, 0, seg.kv_head);
     const size_t value_region = region_offset(geo, 1, seg.kv_head);
     const int page_tokens = geo.page_tokens;
-    // Step s covers block list[s] under KV page activation, block s otherwise; keys at or past key_limit are masked.
+    // Step s covers keys 64 s .. of block s, or under KV page activation the activation page from key list[s] (the
+    // 64-key block holding it is read, its other keys masked); keys at or past key_limit are masked.
     const int32_t* list = seg.list >= 0 ? a.lists + seg.list : nullptr;
     const int key_limit = list != nullptr ? seg.position + 1 : seg.key_end;
     const int step_end = (seg.key_end + kStepKeys - 1) / kStepKeys;
 
     for (int step = seg.key_begin / kStepKeys; step < step_end; ++step) {
-        const int key0 = (list != nullptr ? load_uniform(list + step) : step) * kStepKeys;
+        const int entry = list != nullptr ? load_uniform(list + step) : step * kStepKeys;
+        const int key0 = entry & ~(kStepKeys - 1);
+        const int key_low = list != nullptr ? entry : 0;
+        const int key_end = list != nullptr ? min(entry + geo.summary_keys, key_limit) : key_limit;
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
         const float* page =
@@ -421,7 +436,9 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int key = key0 + 16 * t + 4 * g + i;
-                scores[t][i] = key < key_limit ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
+                const bool visible =
+                    static_cast<uint32_t>(key - key_low) < static_cast<uint32_t>(key_end - key_low);
+                scores[t][i] = visible ? scores[t][i] * a.scale_log2 : kNegativeInfinity;
             }
         }
         const float alpha = softmax_step(scores, state.maximum, state.sum);

@@ -306,8 +306,9 @@ struct SynapseKvCache {
     uint32_t fused_sums = 1;     // decoder: 1 adds deferred slice sums in the consuming kernels
     uint32_t segment_cost = 8;   // quarter key steps a decode worker's range pays for each row start in it
     SynapseKvPageActivation activation{};  // KV page activation (enabled = 0: dense)
-    synapse_kv::DeviceBuffer<uint8_t> summaries;  // per pool page: key minima and maxima of its 64-key blocks
+    synapse_kv::DeviceBuffer<uint8_t> summaries;  // per pool page: key minima and maxima of its activation pages
     uint64_t summary_page_bytes = 0;
+    int32_t summary_keys = 64;  // positions per activation page the summaries are kept for
 
     // Host shadow of the allocator (same rules as the table kernel).
     std::vector<uint32_t> capacity;
@@ -589,6 +590,7 @@ Geometry geometry(const SynapseKvCache& cache, uint32_t layer) {
     g.group = static_cast<int32_t>(cache.dims.heads / cache.dims.kv_heads);
     g.head_dim = static_cast<int32_t>(cache.dims.head_dim);
     g.layer = static_cast<int32_t>(layer);
+    g.summary_keys = cache.summary_keys;
     return g;
 }
 
@@ -704,10 +706,10 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     }
 
     // KV page activation (Qwen2KvPageMasks.cs:21-54): a decode unit is a token before the prompt boundary that is
-    // alone in its slot. KvPageSelector.Select (KvPageSelector.cs:17-54) with 64-position pages gives its row, per
-    // KV head, the sink block 0, `budget` blocks of 1 .. candidates (ranked by key bound on the device, or drawn
-    // here) and the window blocks window_page .. position / 64; when the budget covers every candidate the row is
-    // dense. Listed rows read their blocks through the decode kernel and take no part in shared-prefix sets.
+    // alone in its slot. KvPageSelector.Select (KvPageSelector.cs:17-54) with pages of P = 16, 32 or 64 positions
+    // gives its row, per KV head, the sink page 0, `budget` pages of 1 .. candidates (ranked by key bound on the
+    // device, or drawn here) and the window pages window_page .. position / P; when the budget covers every candidate
+    // the row is dense. Each page is one decode step (its 64-key block read, the keys outside the page masked). Listed rows read their blocks through the decode kernel and take no part in shared-prefix sets.
     struct Unit {
         int32_t window_page;  // -1: dense
         int32_t candidates;
@@ -726,7 +728,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             }
             const int64_t keys = static_cast<int64_t>(tokens[index].position) + 1;
             const int32_t window_page =
-                static_cast<int32_t>(std::max<int64_t>(0, keys - activation.window_tokens) / kStepKeys);
+                static_cast<int32_t>(std::max<int64_t>(0, keys - activation.window_tokens) / cache.summary_keys);
             const int32_t candidates = std::max(0, window_page - 1);
             if (static_cast<uint32_t>(candidates) <= activation.budget_pages) {
                 continue;
@@ -736,7 +738,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
                                                  std::to_string(kMaxSelectCandidates) + " pages; token " +
                                                  std::to_string(index) + " has " + std::to_string(candidates));
             }
-            const int32_t own_page = tokens[index].position / kStepKeys;
+            const int32_t own_page = tokens[index].position / cache.summary_keys;
             units[index] = Unit{window_page, candidates,
                                 1 + static_cast<int32_t>(activation.budget_pages) + own_page - window_page + 1};
         }
@@ -819,7 +821,8 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         }
     }
 
-    // Block lists: [sink block 0][budget blocks, ascending][window blocks]. Key-bound budget entries are written by
+    // Lists of pages' first keys: [sink page 0][budget pages, ascending][window pages]. Key-bound budget entries are
+    // written by
     // the selection kernel of each layer (one list region serves every layer); random draws depend on the layer
     // (seed = Seed * 1000003 + layer * 7919 + kv_head * 104729 + position, Qwen2KvPageMasks.cs:37, in 32-bit
     // wrap-around), so each layer gets its own region.
@@ -838,9 +841,10 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         const int32_t position = tokens[row.token].position;
         for (uint32_t layer = 0; layer < list_layers; ++layer) {
             int32_t* list = &lists[static_cast<size_t>(layer) * list_entries + row.list];
+            const int32_t size = cache.summary_keys;
             list[0] = 0;
-            for (int32_t page = unit.window_page; page <= position / kStepKeys; ++page) {
-                list[1 + budget + page - unit.window_page] = page;
+            for (int32_t page = unit.window_page; page <= position / size; ++page) {
+                list[1 + budget + page - unit.window_page] = page * size;
             }
             if (random) {
                 // RandomPages (KvPageSelector.cs:118-129): a partial Fisher-Yates draw over pages 1..candidates.
@@ -855,7 +859,9 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
                     std::swap(drawn[index], drawn[generator.next(index, unit.candidates)]);
                 }
                 std::sort(drawn.begin(), drawn.begin() + budget);
-                std::copy(drawn.begin(), drawn.begin() + budget, list + 1);
+                for (int32_t index = 0; index < budget; ++index) {
+                    list[1 + index] = drawn[index] * size;
+                }
             }
         }
         if (!random) {
@@ -878,7 +884,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             const uint32_t position = static_cast<uint32_t>(tokens[index].position);
             const int32_t page = cache.table[static_cast<size_t>(tokens[index].slot) * dims.pages_per_slot +
                                              position / dims.page_tokens];
-            return static_cast<int64_t>(page) * 65536 + (position % dims.page_tokens) / kStepKeys;
+            return static_cast<int64_t>(page) * 65536 + (position % dims.page_tokens) / cache.summary_keys;
         };
         std::vector<int64_t> keys(count);
         for (int32_t index = 0; index < count; ++index) {
@@ -903,14 +909,15 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             const int64_t position = tokens[index].position;
             const auto range = std::equal_range(sorted.begin(), sorted.end(), keys[index]);
             const bool solo = range.second - range.first == 1 && in_slot[slot] == 1;
-            if (solo && (position % kStepKeys == 0 || position == cache.fold_next[slot])) {
+            const int64_t size = cache.summary_keys;
+            if (solo && (position % size == 0 || position == cache.fold_next[slot])) {
                 extend[index] = 1;
             } else {
-                const int64_t start = position / kStepKeys * kStepKeys;
+                const int64_t start = position / size * size;
                 recompute.emplace_back(keys[index],
-                                       static_cast<int32_t>(std::min<int64_t>(kStepKeys, cache.length[slot] - start)));
+                                       static_cast<int32_t>(std::min<int64_t>(size, cache.length[slot] - start)));
                 const Unit& unit = units[index];
-                if (unit.window_page >= 0 && unit.window_page - 1 >= static_cast<int32_t>(position / kStepKeys)) {
+                if (unit.window_page >= 0 && unit.window_page - 1 >= static_cast<int32_t>(position / size)) {
                     select_reads_touched = true;
                 }
             }
@@ -1878,12 +1885,8 @@ int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPag
     return guarded([&] {
         const SynapseKvPageActivation wanted = *activation;
         if (wanted.enabled != 0) {
-            // KvPageActivation.Validate (KvPageActivation.cs:23-37); 16- and 32-position pages are not built here.
-            if (wanted.page_tokens == 16 || wanted.page_tokens == 32) {
-                fail(SYNAPSE_KV_UNAVAILABLE, "KV page activation selects 64-position pages here (" +
-                                                 std::to_string(wanted.page_tokens) + " requested)");
-            }
-            if (wanted.page_tokens != 64) {
+            // KvPageActivation.Validate (KvPageActivation.cs:23-37).
+            if (wanted.page_tokens != 16 && wanted.page_tokens != 32 && wanted.page_tokens != 64) {
                 invalid("KV pages hold 16, 32, or 64 positions");
             }
             if (wanted.selection != SYNAPSE_KV_SELECT_KEY_BOUND && wanted.selection != SYNAPSE_KV_SELECT_RANDOM) {
@@ -1895,11 +1898,14 @@ int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPag
         }
         set_device(*cache);
         cache->step_ready = false;
-        const bool rebuild = wanted.enabled != 0 && cache->activation.enabled == 0;
-        if (wanted.enabled != 0 && cache->summaries.pointer == nullptr) {
+        // Summaries are rebuilt when activation is switched on or its page size changes.
+        const bool rebuild = wanted.enabled != 0 && (cache->activation.enabled == 0 ||
+                                                     static_cast<int32_t>(wanted.page_tokens) != cache->summary_keys);
+        if (rebuild) {
             const Dims& dims = cache->dims;
+            cache->summary_keys = static_cast<int32_t>(wanted.page_tokens);
             cache->summary_page_bytes =
-                summary_page_elements(dims.layers, dims.kv_heads, dims.page_tokens, dims.head_dim) *
+                summary_page_elements(dims.layers, dims.kv_heads, dims.page_tokens, dims.head_dim, cache->summary_keys) *
                 (dims.precision == SYNAPSE_KV_F16 ? 2 : 4);
             cache->summaries.ensure(cache->summary_page_bytes * dims.max_pages, "key summaries");
         }
@@ -1910,10 +1916,10 @@ int32_t synapse_kv_set_page_activation(SynapseKvCache* cache, const SynapseKvPag
             std::vector<int32_t> blocks;
             for (uint32_t page = 0; page < dims.max_pages; ++page) {
                 if (cache->refcount[page] > 0) {
-                    for (uint32_t block = 0; block < dims.page_tokens / kStepKeys; ++block) {
+                    for (int32_t block = 0; block < static_cast<int32_t>(dims.page_tokens) / cache->summary_keys; ++block) {
                         blocks.push_back(static_cast<int32_t>(page));
-                        blocks.push_back(static_cast<int32_t>(block));
-                        blocks.push_back(kStepKeys);
+                        blocks.push_back(block);
+                        blocks.push_back(cache->summary_keys);
                     }
                 }
             }
@@ -2259,10 +2265,11 @@ void import_rows(SynapseKvCache& cache, uint32_t slot, const SynapseKvPrefixHead
     if (cache.activation.enabled != 0) {
         // Key summaries of the imported blocks (the keys below the length).
         std::vector<int32_t> blocks;
-        for (uint32_t position = 0; position < header.length; position += kStepKeys) {
+        const uint32_t size = static_cast<uint32_t>(cache.summary_keys);
+        for (uint32_t position = 0; position < header.length; position += size) {
             blocks.push_back(slot_page(cache, slot, position / dims.page_tokens));
-            blocks.push_back(static_cast<int32_t>((position % dims.page_tokens) / kStepKeys));
-            blocks.push_back(static_cast<int32_t>(std::min<uint32_t>(kStepKeys, header.length - position)));
+            blocks.push_back(static_cast<int32_t>((position % dims.page_tokens) / size));
+            blocks.push_back(static_cast<int32_t>(std::min<uint32_t>(size, header.length - position)));
         }
         const size_t blob = blocks.size() * sizeof(int32_t);
         cache.op_blob.ensure(blob, "operation buffer");

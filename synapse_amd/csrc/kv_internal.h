@@ -56,8 +56,8 @@ struct PageArgs {
 
 // A decode segment: keys [key_begin, key_end) of one (token, KV head) row. `row` >= 0 is the segment's partial
 // row and `merge` the row's merge entry; row -1 writes the normalized output directly. With list >= 0 the row
-// attends the 64-key blocks lists[list + 0 ..] (KV page activation) and key_begin / key_end count list entries
-// times 64. `last` marks the piece that holds the row's own position (the fused append writes it first).
+// attends the activation pages whose first keys are lists[list + 0 ..] (KV page activation: a step reads the 64-key
+// block holding the page and masks the keys outside it) and key_begin / key_end count list entries times 64. `last` marks the piece that holds the row's own position (the fused append writes it first).
 struct DecodeSegment {
     int32_t token;
     int32_t kv_head;
@@ -112,6 +112,7 @@ struct Geometry {
     int32_t group;
     int32_t head_dim;
     int32_t layer;
+    int32_t summary_keys;  // KV page activation: positions per activation page (16, 32 or 64), one summary each
 };
 
 struct AppendArgs {
@@ -124,9 +125,9 @@ struct AppendArgs {
     const float* cosines;
     const float* sines;
     int32_t write_back;  // 1: rotated Q and K replace the qkv values; 0: qkv is left as it was
-    // KV page activation: a token with extend[token] != 0 is alone in its 64-key block in the step and appends
-    // right after its slot's keys, whose block summary covers exactly the keys below it, so the append kernel folds
-    // the new key in (or starts the summary at a block's first position). Other written blocks are recomputed from
+    // KV page activation: a token with extend[token] != 0 is alone in its activation page in the step and appends
+    // right after its slot's keys, whose page summary covers exactly the keys below it, so the append kernel folds
+    // the new key in (or starts the summary at a page's first position). Other written blocks are recomputed from
     // their keys below the slot's new length. Null: no summaries.
     uint8_t* summaries;
     uint64_t summary_page_bytes;
@@ -201,13 +202,14 @@ struct ProjectionArgs {
 };
 
 // KV page activation (ADR-016). Key summaries live in their own buffer, one summary page per pool page:
-// [layer][kv_head][64-key block of the page][min, max][head_dim] in the storage type (exact minima and maxima of the
-// stored keys).
-inline uint64_t summary_page_elements(int layers, int kv_heads, int page_tokens, int head_dim) {
-    return static_cast<uint64_t>(layers) * kv_heads * (page_tokens / 64) * 2 * head_dim;
+// [layer][kv_head][activation page of the pool page][min, max][head_dim] in the storage type (exact minima and
+// maxima of the stored keys). An activation page is summary_keys (16, 32 or 64) consecutive positions.
+inline uint64_t summary_page_elements(int layers, int kv_heads, int page_tokens, int head_dim, int summary_keys) {
+    return static_cast<uint64_t>(layers) * kv_heads * (page_tokens / summary_keys) * 2 * head_dim;
 }
 
-// Recomputes the summaries of `count` (pool page, 64-key block of the page, keys 1..64) items for layers
+// Recomputes the summaries of `count` (pool page, activation page of the pool page, keys 1..summary_keys) items for
+// layers
 // [first_layer, first_layer + layers) and every KV head from the block's first `keys` stored keys.
 struct SummaryArgs {
     Geometry geo;  // geo.layer unused
@@ -220,9 +222,11 @@ struct SummaryArgs {
     int32_t pad;
 };
 
-// One key-bound selection: the row (token, kv_head) ranks blocks 1..candidates of its slot and writes the `budget`
-// best (ascending) to lists[list + 1 ..] (lists[list] is the sink block, the window blocks follow the budget).
-constexpr int kMaxSelectCandidates = 4096;  // blocks one key-bound selection ranks (262,144 positions)
+// One key-bound selection: the row (token, kv_head) ranks activation pages 1..candidates of its slot and writes the
+// first keys of the `budget` best (ascending) to lists[list + 1 ..] (lists[list] is the sink page, the window pages
+// follow the budget). The last tile's merge holds up to 128 tiles' kept keys in LDS: 8,192 candidates (131,072
+// positions with 16-position pages, 524,288 with 64).
+constexpr int kMaxSelectCandidates = 8192;
 struct SelectJob {
     int32_t token;
     int32_t kv_head;

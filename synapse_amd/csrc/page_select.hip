@@ -1,21 +1,22 @@
-// Query-aware KV page activation (ADR-016) on the device: per-block key summaries and key-bound page selection.
+// Query-aware KV page activation (ADR-016) on the device: per-page key summaries and key-bound page selection.
 //
-// Semantics: KvPageSelector (src/Synapse.Runtime/Features/TextGeneration/KvPageSelector.cs:17-54) with 64-position
-// pages. PageBound (:57-87): per channel the minimum and maximum of the page's keys (MathF.Min / MathF.Max from the
-// first key on), then for each query head of the group bound = sum over channels, in order, of
+// Semantics: KvPageSelector (src/Synapse.Runtime/Features/TextGeneration/KvPageSelector.cs:17-54) with pages of
+// 16, 32 or 64 positions (KvPageActivation.PageTokens, KvPageActivation.cs:12-13, 33-36). PageBound (:57-87): per
+// channel the minimum and maximum of the page's keys (MathF.Min / MathF.Max from the first key on), then for each query head of the group bound = sum over channels, in order, of
 // MathF.Max(q_c * min_c, q_c * max_c) (products and sums rounded separately), and the page's bound is the maximum
 // over the heads. BestPages (:90-107): candidates 1..windowPage - 1 ranked by bound, highest first, ties to the
 // earlier page (float.CompareTo order: NaN below every number), the first `budget` taken.
 //
-// MI355X mapping: summaries are kept per (pool page, layer, KV head, 64-key block) in the storage type (exact), so a
-// bound reads 2 * head_dim values per block instead of its 64 keys. The append kernel recomputes the summary of a
-// block it alone writes in the step; summary_kernel covers the blocks several tokens of the step write (prompt
+// MI355X mapping: summaries are kept per (pool page, layer, KV head, activation page) in the storage type (exact),
+// so a bound reads 2 * head_dim values per page instead of its keys. The append kernel folds a key into the summary
+// of a page it alone writes in the step; summary_kernel covers the pages several tokens of the step write (prompt
 // runs) and everything cached when activation is switched on. Selection is one launch: select_kernel spreads
-// (selection job, 64 candidate blocks) tiles over the whole device, staging the tile's summaries (widened) and the
+// (selection job, 64 candidate pages) tiles over the whole device, staging the tile's summaries (widened) and the
 // rotated query heads in LDS; one thread per (candidate, query head) sums the channels in the reference's order,
 // so bounds are bit-identical with the CPU path. Each tile keeps its best min(budget, 64) candidates (rank keys:
-// bound descending, then the earlier block); the last tile of a job to finish (an agent-scope counter per job,
-// after a release fence) ranks the kept keys and writes the selected blocks, ascending, into the row's block list.
+// bound descending, then the earlier page); the last tile of a job to finish (an agent-scope counter per job,
+// after a release fence) ranks the kept keys and writes the selected pages' first keys, ascending, into the row's
+// list. The decode kernel reads the 64-key block holding each listed page and masks the keys outside the page.
 
 #include "page_summary.h"
 
@@ -31,8 +32,8 @@ __device__ inline void rotate_pair(float x, float y, float c, float s, float& fi
     second = x * s + y * c;
 }
 
-// Grid (items, layers, kv_heads) of 256 threads: the summary of one (page, block, keys) item's first keys, layer and
-// KV head.
+// Grid (items, layers, kv_heads) of 256 threads: the summary of one (pool page, activation page, keys) item's first
+// keys, layer and KV head.
 template <typename T>
 __global__ __launch_bounds__(256) void summary_kernel(SummaryArgs a) {
     __shared__ SummaryScratch<T> scratch;
@@ -41,18 +42,45 @@ __global__ __launch_bounds__(256) void summary_kernel(SummaryArgs a) {
                        a.summary_page_bytes, scratch);
 }
 
-// Sort key of a candidate, 44 bits: ascending order = bound descending (float.CompareTo: NaN below every number, -0
-// equal to +0), then block ascending (KvPageSelector.cs:112-113). Keys are distinct (the block index is part).
+// Sort key of a candidate: ascending order = bound descending (float.CompareTo: NaN below every number, -0 equal to
+// +0), then page ascending (KvPageSelector.cs:112-113). Keys are distinct (the page index is the low 32 bits).
 __device__ inline uint64_t rank_key(float bound, int index) {
     uint32_t ordered = 0;  // NaN: after every number
     if (bound == bound) {
         const uint32_t bits = __float_as_uint(bound == 0.0f ? 0.0f : bound);
         ordered = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);  // ascending with the value, never 0
     }
-    return (static_cast<uint64_t>(~ordered) << 12) | static_cast<uint32_t>(index);
+    return (static_cast<uint64_t>(~ordered) << 32) | static_cast<uint32_t>(index);
 }
 
-// Elements of one staged candidate row: the block's minimum row, its maximum row, and 16 bytes of padding (rows at
+__host__ __device__ constexpr int next_power_of_two(int value) {
+    int power = 1;
+    while (power < value) {
+        power <<= 1;
+    }
+    return power;
+}
+
+// Ascending bitonic sort of `count` (a power of two) keys in LDS by the whole workgroup; ends with a barrier.
+__device__ void bitonic_sort(uint64_t* keys, int count) {
+    for (int size = 2; size <= count; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int pair = threadIdx.x; pair < count / 2; pair += blockDim.x) {
+                const int low = 2 * pair - (pair & (stride - 1));
+                const int high = low + stride;
+                const uint64_t first = keys[low];
+                const uint64_t second = keys[high];
+                if ((first > second) == ((low & size) == 0)) {
+                    keys[low] = second;
+                    keys[high] = first;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Elements of one staged candidate row: the page's minimum row, its maximum row, and 16 bytes of padding (rows at
 // a 16-byte stride that spreads the lanes of a wave over the LDS banks).
 template <typename T>
 __host__ __device__ constexpr int staged_row(int head_dim) {
@@ -60,11 +88,11 @@ __host__ __device__ constexpr int staged_row(int head_dim) {
 }
 
 // Dynamic LDS of the select kernel: the largest of the tile's staged summaries, a summary work item's scratch, and
-// the last tile's merge (kept keys, then the chosen block of each rank).
+// the last tile's merge (kept keys, padded to a power of two for the sort).
 template <typename T>
-size_t select_shared_bytes(int head_dim, int merged, int budget) {
+size_t select_shared_bytes(int head_dim, int merged) {
     const size_t tile = static_cast<size_t>(kTileCandidates) * staged_row<T>(head_dim) * sizeof(T);
-    const size_t merge = static_cast<size_t>(merged) * sizeof(uint64_t) + static_cast<size_t>(budget) * sizeof(int32_t);
+    const size_t merge = static_cast<size_t>(next_power_of_two(merged)) * sizeof(uint64_t);
     size_t bytes = sizeof(SummaryScratch<T>);
     bytes = tile > bytes ? tile : bytes;
     return merge > bytes ? merge : bytes;
@@ -80,7 +108,7 @@ __device__ inline float best_bound(const float* head_bounds, int group, int cand
     return best;
 }
 
-// Grid (tiles, jobs) of 64 * group threads: the bounds of candidate blocks 64 * tile + 1 .. 64 * tile + 64 of one
+// Grid (tiles, jobs) of 64 * group threads: the bounds of candidate pages 64 * tile + 1 .. 64 * tile + 64 of one
 // job. Thread (head h = tid / 64, candidate c = tid % 64) sums MathF.Max(q * min, q * max) over channels in order
 // (one rounding per product and per sum); the candidate's bound is the MathF.Max over heads in order
 // (KvPageSelector.cs:79-92). Each tile keeps its best min(budget, 64) rank keys (the job's best `budget` are among
@@ -118,7 +146,7 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     // 1. The pool pages of the tile's candidates (one table load each).
     const int32_t* table = g.block_table + static_cast<size_t>(token.slot) * g.pages_per_slot;
     if (threadIdx.x < count) {
-        pages[threadIdx.x] = table[((first + threadIdx.x + 1) * kBlockKeys) / g.page_tokens];
+        pages[threadIdx.x] = table[((first + threadIdx.x + 1) * g.summary_keys) / g.page_tokens];
     }
     // 2. The group's query heads, rotated at the token's position when Q in qkv is unrotated.
     const float* row = a.qkv + static_cast<size_t>(job.token) * a.qkv_stride + static_cast<size_t>(job.kv_head) * group * d;
@@ -149,10 +177,10 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
             const int item = batch + threadIdx.x + round * blockDim.x;
             if (item < items) {
                 const int candidate = item / row_chunks;
-                const int key = (first + candidate + 1) * kBlockKeys;
+                const int key = (first + candidate + 1) * g.summary_keys;
                 const T* summary = reinterpret_cast<const T*>(a.summaries +
                                                               static_cast<uint64_t>(pages[candidate]) * a.summary_page_bytes);
-                const size_t at = summary_offset(g, g.layer, job.kv_head, (key % g.page_tokens) / kBlockKeys, 0, 0);
+                const size_t at = summary_offset(g, g.layer, job.kv_head, (key % g.page_tokens) / g.summary_keys, 0, 0);
                 loaded[round] = reinterpret_cast<const uint4*>(summary + at)[item % row_chunks];
             }
         }
@@ -241,27 +269,23 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
         }
         merged += kept;
     }
-    int32_t* chosen = reinterpret_cast<int32_t*>(merged_keys + merged);  // block index of each rank below budget
-    __syncthreads();
-    for (int entry = threadIdx.x; entry < merged; entry += blockDim.x) {
-        const uint64_t mine = merged_keys[entry];
-        int rank = 0;
-        for (int other = 0; other < merged; ++other) {
-            rank += merged_keys[other] < mine ? 1 : 0;
-        }
-        if (rank < a.budget) {
-            chosen[rank] = static_cast<int32_t>(mine & 0xFFF);
-        }
+    // Sorted by rank key (the array padded to a power of two with keys above every real one), the first `budget`
+    // keys are the selected pages; their indices, sorted again in the same space (budget <= merged), give the list
+    // in ascending page order (KvPageSelector marks pages; the list is read in key order).
+    const int padded = next_power_of_two(merged);
+    for (int entry = merged + threadIdx.x; entry < padded; entry += blockDim.x) {
+        merged_keys[entry] = ~0ull;
     }
     __syncthreads();
-    // The chosen blocks in ascending order (KvPageSelector marks pages; the list is read in block order).
+    bitonic_sort(merged_keys, padded);
+    const int chosen = next_power_of_two(a.budget);
+    for (int entry = threadIdx.x; entry < chosen; entry += blockDim.x) {
+        merged_keys[entry] = entry < a.budget ? (merged_keys[entry] & 0xFFFFFFFFull) : ~0ull;
+    }
+    __syncthreads();
+    bitonic_sort(merged_keys, chosen);
     for (int r = threadIdx.x; r < a.budget; r += blockDim.x) {
-        const int index = chosen[r];
-        int before = 0;
-        for (int other = 0; other < a.budget; ++other) {
-            before += chosen[other] < index ? 1 : 0;
-        }
-        a.lists[job.list + 1 + before] = index + 1;
+        a.lists[job.list + 1 + r] = (static_cast<int32_t>(merged_keys[r]) + 1) * g.summary_keys;
     }
 }
 
@@ -303,10 +327,10 @@ hipError_t launch_select(const Launch& launch, const SelectArgs& args, int most_
         return configured;
     }
     if (fp16) {
-        const size_t shared = select_shared_bytes<_Float16>(args.geo.head_dim, merged, args.budget);
+        const size_t shared = select_shared_bytes<_Float16>(args.geo.head_dim, merged);
         SYNAPSE_KV_LAUNCH_SHARED(select_kernel<_Float16>, grid, block, shared, launch, args);
     } else {
-        const size_t shared = select_shared_bytes<float>(args.geo.head_dim, merged, args.budget);
+        const size_t shared = select_shared_bytes<float>(args.geo.head_dim, merged);
         SYNAPSE_KV_LAUNCH_SHARED(select_kernel<float>, grid, block, shared, launch, args);
     }
     return hipGetLastError();

@@ -1,6 +1,6 @@
-// Key summaries of KV page activation (ADR-016): per (pool page, layer, KV head, 64-key block) the per-channel
-// minimum and maximum of the block's keys below the writing slot's length, kept in the storage type (exact). KvPageSelector.PageBound
-// (src/Synapse.Runtime/Features/TextGeneration/KvPageSelector.cs:57-78) reduces the page's keys with MathF.Min and
+// Key summaries of KV page activation (ADR-016): per (pool page, layer, KV head, activation page of 16, 32 or 64
+// positions) the per-channel minimum and maximum of the page's keys below the writing slot's length, kept in the
+// storage type (exact). KvPageSelector.PageBound (src/Synapse.Runtime/Features/TextGeneration/KvPageSelector.cs:57-78) reduces the page's keys with MathF.Min and
 // MathF.Max; both are exact and, for the non-NaN values keys hold, independent of the order of the keys.
 #pragma once
 
@@ -41,9 +41,9 @@ __device__ inline float widen(T value) {
     return static_cast<float>(value);
 }
 
-// Element offset of (layer, kv_head, block of the page, min|max, channel) in a summary page.
+// Element offset of (layer, kv_head, activation page of the pool page, min|max, channel) in a summary page.
 __device__ inline size_t summary_offset(const Geometry& g, int layer, int kv_head, int block, int which, int channel) {
-    const int blocks = g.page_tokens / kBlockKeys;
+    const int blocks = g.page_tokens / g.summary_keys;
     return ((((static_cast<size_t>(layer) * g.kv_heads + kv_head) * blocks + block) * 2 + which) * g.head_dim) + channel;
 }
 
@@ -55,17 +55,20 @@ struct SummaryScratch {
     float partial[2][512];
 };
 
-// Summary of the first `valid` (1..64) keys of block `block` of pool page `page` (layer, kv_head), by the whole
-// workgroup (blockDim.x a multiple of 64, at most 512): the block's keys are copied to LDS with 16-byte loads, the
-// keys of each channel are reduced in shares of 64 / shares keys, and the shares combined. Starts and ends with a
-// barrier.
+// Summary of the first `valid` (1..summary_keys) keys of activation page `block` of pool page `page` (layer,
+// kv_head), by the whole workgroup (blockDim.x a multiple of 64, at most 512): the 64-key block holding the page is
+// copied to LDS with 16-byte loads, the page's keys of each channel are reduced in shares, and the shares combined.
+// Starts and ends with a barrier.
 template <typename T>
 __device__ void summarize_block(const Geometry& g, int layer, int kv_head, int page, int block, int valid,
                                 uint8_t* summaries, uint64_t summary_page_bytes, SummaryScratch<T>& scratch) {
     const int d = g.head_dim;
     const T* region = reinterpret_cast<const T*>(g.pool + static_cast<uint64_t>(page) * g.page_bytes) +
                       ((static_cast<size_t>(layer) * 2) * g.kv_heads + kv_head) * static_cast<size_t>(g.page_tokens) * d;
-    const uint4* source = reinterpret_cast<const uint4*>(region + static_cast<size_t>(block) * kBlockKeys * d);
+    const int first_key = block * g.summary_keys;  // within the pool page
+    const int offset = first_key % kBlockKeys;     // within its 64-key block
+    const uint4* source =
+        reinterpret_cast<const uint4*>(region + static_cast<size_t>(first_key / kBlockKeys) * kBlockKeys * d);
     uint4* staged = reinterpret_cast<uint4*>(scratch.keys);
     const int chunks = kBlockKeys * d * static_cast<int>(sizeof(T)) / 16;
     __syncthreads();
@@ -75,7 +78,7 @@ __device__ void summarize_block(const Geometry& g, int layer, int kv_head, int p
     __syncthreads();
     const int fit = static_cast<int>(blockDim.x) / d;  // the keys of a channel are split into 1, 2 or 4 runs
     const int shares = fit >= 4 ? 4 : (fit >= 2 ? 2 : 1);
-    const int per_share = kBlockKeys / shares;
+    const int per_share = g.summary_keys / shares;
     for (int item = threadIdx.x; item < d * shares; item += blockDim.x) {
         const int channel = item % d;
         const int share = item / d;
@@ -84,7 +87,7 @@ __device__ void summarize_block(const Geometry& g, int layer, int kv_head, int p
         float maximum = -__builtin_inff();
         const int stop = min((share + 1) * per_share, valid);
         for (int key = share * per_share; key < stop; ++key) {
-            const float value = widen(scratch.keys[key_offset<T>(d, key, channel)]);
+            const float value = widen(scratch.keys[key_offset<T>(d, offset + key, channel)]);
             minimum = math_min(minimum, value);
             maximum = math_max(maximum, value);
         }

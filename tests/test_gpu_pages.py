@@ -31,9 +31,9 @@ class PagePair(Pair):
         self.maximum = kwargs.get("max_positions", 4096)
         self.activation = None
 
-    def activate(self, budget, window, selection="key_bound", seed=0):
-        self.gpu.set_page_activation(budget, window, selection=selection, seed=seed)
-        self.activation = (budget, window, 64, 0 if selection == "key_bound" else 1, seed)
+    def activate(self, budget, window, selection="key_bound", seed=0, page_tokens=64):
+        self.gpu.set_page_activation(budget, window, page_tokens=page_tokens, selection=selection, seed=seed)
+        self.activation = (budget, window, page_tokens, 0 if selection == "key_bound" else 1, seed)
 
     def deactivate(self):
         self.gpu.set_page_activation(None)
@@ -199,14 +199,12 @@ def test_prompt_tokens_stay_dense(torch_gpu):
 
 
 def test_page_activation_arguments(torch_gpu):
-    from synapse_amd import InvalidOperationError, NotSupportedError, PagedKvCache
+    from synapse_amd import InvalidOperationError, PagedKvCache
     from synapse_amd.native import PageActivation
 
     say("page activation arguments")
     cache = PagedKvCache(layers=1, heads=14, kv_heads=2, head_dim=64, max_positions=512, growth_positions=256,
                          page_tokens=64, precision="f16", session_slots=1, step_tokens=8, max_pages=8)
-    with pytest.raises(NotSupportedError, match="64-position"):
-        cache.set_page_activation(1, 64, page_tokens=16)
     with pytest.raises(InvalidOperationError, match="16, 32, or 64"):
         cache.set_page_activation(1, 64, page_tokens=24)
     with pytest.raises(ValueError):
@@ -259,5 +257,63 @@ def test_folded_summaries_through_block_ends_and_truncation(torch_gpu):
         pair.run([(0, position)], rng, expect_sparse=True)
     pair.run([(0, 470), (0, 471)], rng, prompt_start=0)
     for position in range(472, 480):
+        pair.run([(0, position)], rng, expect_sparse=True)
+    pair.check_contents(0)
+
+
+SMALL_PAGE_SHAPES = [
+    # (heads, kv_heads, head_dim, precision, page)
+    (28, 4, 128, "f16", 256),
+    (14, 2, 64, "f32", 64),
+    (8, 8, 128, "f16", 128),
+]
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,precision,page", SMALL_PAGE_SHAPES)
+@pytest.mark.parametrize("activation_page", [16, 32])
+@pytest.mark.parametrize("selection", ["key_bound", "random"])
+def test_small_activation_pages(torch_gpu, heads, kv_heads, head_dim, precision, page, activation_page, selection):
+    """KvPageActivation.PageTokens 16 and 32 (KvPageActivation.cs:12-13, 33-36): summaries per 16- or 32-position
+    page, selection over those pages, and decode steps that read a listed page's 64-key block with the keys outside
+    the page masked. Windows that end inside a 64-key block, a budget past one tile of 64 candidates, a slot with
+    two tokens and a token past the prompt boundary; then the page size changes while activation stays on (the
+    summaries are rebuilt) and back."""
+    say("small activation pages", heads, kv_heads, head_dim, precision, page, activation_page, selection)
+    pair = PagePair(torch_gpu, heads=heads, kv_heads=kv_heads, head_dim=head_dim, precision=precision, page=page,
+                    growth=256, max_positions=4096, slots=4, max_pages=4096 // page * 4 + 8)
+    rng = np.random.default_rng(head_dim + heads + activation_page + len(selection))
+    prefill(pair, rng, [(0, 2500), (1, 900), (2, 300)])
+    pair.activate(3, 40, selection=selection, seed=5, page_tokens=activation_page)
+    pair.run([(0, 2500), (1, 900), (2, 300)], rng, expect_sparse=True)
+    pair.run([(0, 2501), (1, 901), (1, 902), (2, 301)], rng, prompt_start=3, expect_sparse=True)
+    pair.activate(70, 100, selection=selection, seed=-7, page_tokens=activation_page)
+    pair.run([(0, 2502), (1, 903)], rng, expect_sparse=True)
+    pair.run([(0, 2503), (1, 904), (2, 302)], rng, fused=True, expect_sparse=True)
+    other = 48 - activation_page  # 16 <-> 32
+    pair.activate(4, 0, selection=selection, page_tokens=other)
+    pair.run([(0, 2504), (1, 905)], rng, expect_sparse=True)
+    pair.activate(2, 17, selection=selection, page_tokens=activation_page)
+    for position in range(2505, 2525):
+        pair.run([(0, position), (1, position - 1600)], rng, expect_sparse=True)
+    pair.check_contents(0)
+
+
+@pytest.mark.parametrize("activation_page", [16, 32])
+def test_small_page_folds_through_page_ends_and_truncation(torch_gpu, activation_page):
+    """One token per step with no window: each completed 16- or 32-position page is a candidate at once, its
+    summary folded key by key from the page's first position; a truncation inside a page and a two-token step make
+    the next append recompute, then folding resumes."""
+    say("small page folds", activation_page)
+    pair = PagePair(torch_gpu, page=128, max_positions=1024, slots=2, max_pages=24)
+    rng = np.random.default_rng(80 + activation_page)
+    prefill(pair, rng, [(0, 300)])
+    pair.activate(2, 0, page_tokens=activation_page)
+    for position in range(300, 380):
+        pair.run([(0, position)], rng, expect_sparse=True)
+    pair.call("truncate", 0, 357)
+    for position in range(357, 380):
+        pair.run([(0, position)], rng, expect_sparse=True)
+    pair.run([(0, 380), (0, 381)], rng, prompt_start=0)
+    for position in range(382, 400):
         pair.run([(0, position)], rng, expect_sparse=True)
     pair.check_contents(0)
