@@ -118,7 +118,7 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     extern __shared__ __align__(16) uint8_t scratch[];
     __shared__ __align__(16) float query[kMaxGroup * 128];
     __shared__ float head_bounds[kMaxGroup * kTileCandidates];
-    __shared__ int32_t pages[kTileCandidates];
+    __shared__ const T* summary_rows[kTileCandidates];
     __shared__ uint64_t tile_keys[kTileCandidates];
     __shared__ int32_t last_tile;
     const Geometry& g = a.geo;
@@ -143,10 +143,14 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     const int group = g.group;
     T* staged = reinterpret_cast<T*>(scratch);  // [candidate][staged_row]: minimum row, maximum row
     const int row_elements = staged_row<T>(d);
-    // 1. The pool pages of the tile's candidates (one table load each).
     const int32_t* table = g.block_table + static_cast<size_t>(token.slot) * g.pages_per_slot;
+    // 1. The summary rows of the tile's candidates (a table load each): minimum and maximum rows, contiguous.
     if (threadIdx.x < count) {
-        pages[threadIdx.x] = table[((first + threadIdx.x + 1) * g.summary_keys) / g.page_tokens];
+        const int key = (first + threadIdx.x + 1) * g.summary_keys;
+        const int page = table[key / g.page_tokens];
+        summary_rows[threadIdx.x] =
+            reinterpret_cast<const T*>(a.summaries + static_cast<uint64_t>(page) * a.summary_page_bytes) +
+            summary_offset(g, g.layer, job.kv_head, (key % g.page_tokens) / g.summary_keys, 0, 0);
     }
     // 2. The group's query heads, rotated at the token's position when Q in qkv is unrotated.
     const float* row = a.qkv + static_cast<size_t>(job.token) * a.qkv_stride + static_cast<size_t>(job.kv_head) * group * d;
@@ -170,28 +174,29 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     const int row_chunks = 2 * d / kPerChunk;
     constexpr int kRounds = 4;
     const int items = count * row_chunks;
+    // Every load is issued (items past the tile clamped to its last one), four into named registers, then stored.
+    static_assert(kRounds == 4, "four named loads");
     for (int batch = 0; batch < items; batch += kRounds * blockDim.x) {
-        uint4 loaded[kRounds];
-#pragma unroll
-        for (int round = 0; round < kRounds; ++round) {
-            const int item = batch + threadIdx.x + round * blockDim.x;
+        auto load = [&](int round) __attribute__((always_inline)) {
+            const int item = min(batch + static_cast<int>(threadIdx.x) + round * static_cast<int>(blockDim.x), items - 1);
+            const int candidate = item / row_chunks;
+            return reinterpret_cast<const uint4*>(summary_rows[candidate])[item - candidate * row_chunks];
+        };
+        auto store = [&](int round, const uint4& value) __attribute__((always_inline)) {
+            const int item = batch + static_cast<int>(threadIdx.x) + round * static_cast<int>(blockDim.x);
             if (item < items) {
                 const int candidate = item / row_chunks;
-                const int key = (first + candidate + 1) * g.summary_keys;
-                const T* summary = reinterpret_cast<const T*>(a.summaries +
-                                                              static_cast<uint64_t>(pages[candidate]) * a.summary_page_bytes);
-                const size_t at = summary_offset(g, g.layer, job.kv_head, (key % g.page_tokens) / g.summary_keys, 0, 0);
-                loaded[round] = reinterpret_cast<const uint4*>(summary + at)[item % row_chunks];
+                reinterpret_cast<uint4*>(staged + candidate * row_elements)[item - candidate * row_chunks] = value;
             }
-        }
-#pragma unroll
-        for (int round = 0; round < kRounds; ++round) {
-            const int item = batch + threadIdx.x + round * blockDim.x;
-            if (item < items) {
-                const int candidate = item / row_chunks;
-                reinterpret_cast<uint4*>(staged + candidate * row_elements)[item % row_chunks] = loaded[round];
-            }
-        }
+        };
+        const uint4 loaded0 = load(0);
+        const uint4 loaded1 = load(1);
+        const uint4 loaded2 = load(2);
+        const uint4 loaded3 = load(3);
+        store(0, loaded0);
+        store(1, loaded1);
+        store(2, loaded2);
+        store(3, loaded3);
     }
     __syncthreads();
     // 3. One (candidate, head) sum per thread.
@@ -207,20 +212,23 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
         // in sign. A zero of either sign added to the running sum leaves it unchanged, since the sum starts at +0
         // and a round-to-nearest sum is -0 only when both addends are -0. Four channels per round, loaded before
         // the serial sum so the LDS reads of a round overlap.
+        // Operands are held in vector registers (a local array written through a cast pointer would live in
+        // scratch memory).
+        typedef T Chunk __attribute__((ext_vector_type(kPerChunk)));
+        typedef float Quad __attribute__((ext_vector_type(4)));
         for (int c0 = 0; c0 < d; c0 += kPerChunk) {
 #pragma clang fp contract(off)
-            T low[kPerChunk];
-            T high[kPerChunk];
-            float qv[kPerChunk];
-            *reinterpret_cast<uint4*>(low) = *reinterpret_cast<const uint4*>(minimum + c0);
-            *reinterpret_cast<uint4*>(high) = *reinterpret_cast<const uint4*>(maximum + c0);
+            const Chunk low = __builtin_bit_cast(Chunk, *reinterpret_cast<const uint4*>(minimum + c0));
+            const Chunk high = __builtin_bit_cast(Chunk, *reinterpret_cast<const uint4*>(maximum + c0));
+            Quad qv[kPerChunk / 4];
 #pragma unroll
-            for (int j = 0; j < kPerChunk; j += 4) {
-                *reinterpret_cast<float4*>(qv + j) = *reinterpret_cast<const float4*>(q + c0 + j);
+            for (int j = 0; j < kPerChunk / 4; ++j) {
+                qv[j] = *reinterpret_cast<const Quad*>(q + c0 + 4 * j);
             }
 #pragma unroll
             for (int j = 0; j < kPerChunk; ++j) {
-                sum += qv[j] * widen(qv[j] >= 0.0f ? high[j] : low[j]);
+                const float value = qv[j / 4][j % 4];
+                sum += value * widen(value >= 0.0f ? high[j] : low[j]);
             }
         }
         head_bounds[head * kTileCandidates + candidate] = sum;
@@ -312,6 +320,15 @@ hipError_t launch_select(const Launch& launch, const SelectArgs& args, int most_
     const dim3 grid(tiles > args.geo.kv_heads ? tiles : args.geo.kv_heads, args.summary_count + args.job_count);
     const dim3 block(kTileCandidates * args.geo.group);
     const int merged = tiles * (args.budget < kTileCandidates ? args.budget : kTileCandidates);
+#ifdef PROBE_PRINT
+    {
+        static int calls = 0;
+        if (calls++ % 97 == 0) {
+            fprintf(stderr, "select grid %u x %u block %u summaries %d jobs %d most %d merged %d\n", grid.x, grid.y,
+                    block.x, args.summary_count, args.job_count, most_candidates, merged);
+        }
+    }
+#endif
     // Dynamic LDS may exceed the 64 KiB default (an FP32 tile at head_dim 128 takes 66,560 bytes).
     static const hipError_t configured = [] {
         constexpr int kMostDynamic = 96 * 1024;
