@@ -1116,6 +1116,10 @@ def main() -> None:
             "unit": "GB/s",
             "frac": round(decode_gbps / PEAK_HBM_GBPS, 4),
             "traffic": traffic["bytes_per_launch"] if traffic else None,
+            # Not measured in this run: read from the committed PMC summary (FETCH_SIZE and WRITE_SIZE runs of their
+            # own, scaled by a 1 GiB copy's counters).
+            "traffic_source": ("profiles/decode_attention_c3_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
+                               "committed summary, not this run)") if traffic else None,
             "algorithmic_bytes_per_launch": int(statistics.mean(decode_bytes)),
             "avg_launch_us": round(decode_seconds * 1e6, 2),
             "timed_launches": decode_launches,
