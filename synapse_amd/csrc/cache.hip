@@ -386,7 +386,6 @@ struct SynapseKvCache {
     bool select_reads_touched = false;  // a selection ranks a block the step writes (window 0 at a block's end)
     int32_t most_candidates = 0;     // largest key-bound selection job
     synapse_kv::DeviceBuffer<uint64_t> select_keys;
-    synapse_kv::DeviceBuffer<int32_t> select_counters;  // zeroed when allocated; the select kernel leaves them 0
 
     ~SynapseKvCache() {
         (void)hipSetDevice(device);
@@ -411,7 +410,6 @@ struct SynapseKvCache {
         partial_ml.reset();
         summaries.reset();
         select_keys.reset();
-        select_counters.reset();
         if (pool != nullptr) {
             (void)hipFree(pool);
         }
@@ -1178,12 +1176,6 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         staging = cache.pageable.acquire(total);
     } else {
         cache.select_keys.ensure(select_jobs.size() * select_key_stride(cache, most_candidates), "page selection keys");
-        if (select_jobs.size() > cache.select_counters.count) {
-            cache.select_counters.ensure(std::max<size_t>(select_jobs.size(), 256), "page selection counters");
-            check_hip(hipMemsetAsync(cache.select_counters.pointer, 0, cache.select_counters.count * sizeof(int32_t),
-                                     cache.stream),
-                      "page selection counters");
-        }
         cache.blob.ensure(total, "step buffer");
         cache.partial_out.ensure(partial_out_floats, "attention partials");
         cache.partial_ml.ensure(partial_ml_floats, "attention partial statistics");
@@ -1545,7 +1537,6 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
         select.jobs = reinterpret_cast<const SelectJob*>(cache.step_blob + cache.select_offset);
         select.lists = lists;
         select.keys = cache.select_keys.pointer;
-        select.counters = cache.select_counters.pointer;
         select.key_stride = static_cast<int32_t>(select_key_stride(cache, cache.most_candidates));
         select.budget = static_cast<int32_t>(cache.activation.budget_pages);
         select.job_count = cache.select_jobs;

@@ -224,7 +224,7 @@ struct SummaryArgs {
 
 // One key-bound selection: the row (token, kv_head) ranks activation pages 1..candidates of its slot and writes the
 // first keys of the `budget` best (ascending) to lists[list + 1 ..] (lists[list] is the sink page, the window pages
-// follow the budget). The last tile's merge holds up to 128 tiles' kept keys in LDS: 8,192 candidates (131,072
+// follow the budget). The per-job merge holds up to 128 tiles' kept keys in LDS: 8,192 candidates (131,072
 // positions with 16-position pages, 524,288 with 64).
 constexpr int kMaxSelectCandidates = 8192;
 struct SelectJob {
@@ -247,8 +247,7 @@ struct SelectArgs {
     uint64_t summary_page_bytes;
     const SelectJob* jobs;
     int32_t* lists;
-    uint64_t* keys;      // [jobs][key_stride]: each tile's best min(budget, 64) rank keys, for the job's last tile
-    int32_t* counters;   // [jobs]: tiles of the job done; zero between launches (the last tile resets it)
+    uint64_t* keys;      // [jobs][key_stride]: each tile's best min(budget, 64) rank keys, merged per job
     int32_t key_stride;  // tiles of the largest job * min(budget, 64)
     int32_t budget;
     int32_t job_count;

@@ -14,9 +14,10 @@
 // (selection job, 64 candidate pages) tiles over the whole device, staging the tile's summaries (widened) and the
 // rotated query heads in LDS; one thread per (candidate, query head) sums the channels in the reference's order,
 // so bounds are bit-identical with the CPU path. Each tile keeps its best min(budget, 64) candidates (rank keys:
-// bound descending, then the earlier page); the last tile of a job to finish (an agent-scope counter per job,
-// after a release fence) ranks the kept keys and writes the selected pages' first keys, ascending, into the row's
-// list. The decode kernel reads the 64-key block holding each listed page and masks the keys outside the page.
+// bound descending, then the earlier page); a second launch, one workgroup per job, sorts the kept keys in LDS and
+// writes the selected pages' first keys, ascending, into the row's list. The decode kernel reads the 64-key block holding each listed page and masks the keys outside the page.
+
+#include <algorithm>
 
 #include "page_summary.h"
 
@@ -87,15 +88,12 @@ __host__ __device__ constexpr int staged_row(int head_dim) {
     return 2 * head_dim + 16 / static_cast<int>(sizeof(T));
 }
 
-// Dynamic LDS of the select kernel: the largest of the tile's staged summaries, a summary work item's scratch, and
-// the last tile's merge (kept keys, padded to a power of two for the sort).
+// Dynamic LDS of the select kernel: the larger of the tile's staged summaries and a summary work item's scratch.
 template <typename T>
-size_t select_shared_bytes(int head_dim, int merged) {
+size_t select_shared_bytes(int head_dim) {
     const size_t tile = static_cast<size_t>(kTileCandidates) * staged_row<T>(head_dim) * sizeof(T);
-    const size_t merge = static_cast<size_t>(next_power_of_two(merged)) * sizeof(uint64_t);
-    size_t bytes = sizeof(SummaryScratch<T>);
-    bytes = tile > bytes ? tile : bytes;
-    return merge > bytes ? merge : bytes;
+    const size_t bytes = sizeof(SummaryScratch<T>);
+    return tile > bytes ? tile : bytes;
 }
 
 // MathF.Max of the candidate's head bounds, heads in order (KvPageSelector.cs:79-92). The head bounds are never
@@ -112,7 +110,7 @@ __device__ inline float best_bound(const float* head_bounds, int group, int cand
 // job. Thread (head h = tid / 64, candidate c = tid % 64) sums MathF.Max(q * min, q * max) over channels in order
 // (one rounding per product and per sum); the candidate's bound is the MathF.Max over heads in order
 // (KvPageSelector.cs:79-92). Each tile keeps its best min(budget, 64) rank keys (the job's best `budget` are among
-// them); the job's last tile merges them.
+// them); select_merge_kernel merges them per job.
 template <typename T>
 __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     extern __shared__ __align__(16) uint8_t scratch[];
@@ -120,7 +118,6 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     __shared__ float head_bounds[kMaxGroup * kTileCandidates];
     __shared__ const T* summary_rows[kTileCandidates];
     __shared__ uint64_t tile_keys[kTileCandidates];
-    __shared__ int32_t last_tile;
     const Geometry& g = a.geo;
     if (static_cast<int>(blockIdx.y) < a.summary_count) {
         // Summary work: pair blockIdx.y of this layer, KV head blockIdx.x.
@@ -234,7 +231,8 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
         head_bounds[head * kTileCandidates + candidate] = sum;
     }
     __syncthreads();
-    // 4. The tile's best min(budget, 64) keys go to keys[job][tile * kept_stride + rank], in rank order.
+    // 4. The tile's best min(budget, 64) keys go to keys[job][tile * kept_stride + rank], in rank order (the job's
+    //    best `budget` are among them; select_merge_kernel merges them).
     if (threadIdx.x < count) {
         tile_keys[threadIdx.x] = rank_key(best_bound(head_bounds, group, threadIdx.x), first + threadIdx.x);
     }
@@ -251,23 +249,103 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
             job_keys[blockIdx.x * kept_stride + rank] = mine;
         }
     }
-    // 5. The job's last tile to finish merges the tiles' keys: the `budget` smallest are the selected blocks.
+}
+
+// Grid (jobs) of kMergeThreads threads, after select_kernel, for jobs of at most kSearchTiles tiles: selects the job's `budget` smallest rank keys among its
+// tiles' kept keys and writes the selected pages' first keys, in ascending page order, to the row's list
+// (KvPageSelector marks pages; the list is read in key order). Each tile's kept keys are sorted (select_kernel
+// writes them by rank), so a key's rank among all of them is the sum over tiles of its lower bound in each (binary
+// search in LDS; keys are distinct, so ranks are exact). A key of rank below `budget` sets its candidate's bit in
+// an LDS bitmap; the bitmap's prefix counts give each selected page its place in the list. A launch of its own: the
+// kernel boundary makes every tile's keys visible, where a last-tile merge inside select_kernel needed a
+// device-scope release per tile and an acquire by the last one (measured: 46.5 against 14.8 us per launch without
+// the merge at 64-position pages).
+constexpr int kMergeThreads = 512;
+constexpr int kBitmapWords = kMaxSelectCandidates / 32;
+
+__global__ __launch_bounds__(kMergeThreads) void select_merge_kernel(SelectArgs a) {
+    extern __shared__ __align__(16) uint8_t scratch[];
+    __shared__ uint32_t bitmap[kBitmapWords];
+    __shared__ uint32_t before[kBitmapWords];
+    const SelectJob job = a.jobs[blockIdx.x];
+    const int tiles = (job.candidates + kTileCandidates - 1) / kTileCandidates;
+    const int kept_stride = min(a.budget, kTileCandidates);
+    const int words = (job.candidates + 31) / 32;
+    const uint64_t* job_keys = a.keys + static_cast<size_t>(blockIdx.x) * a.key_stride;
+    uint64_t* keys = reinterpret_cast<uint64_t*>(scratch);  // [tile][kept_stride], each tile's run sorted
+    auto kept_of = [&](int t) { return min(kept_stride, min(kTileCandidates, job.candidates - t * kTileCandidates)); };
+    for (int e = threadIdx.x; e < tiles * kept_stride; e += blockDim.x) {
+        keys[e] = e % kept_stride < kept_of(e / kept_stride) ? job_keys[e] : ~0ull;
+    }
+    for (int w = threadIdx.x; w < words; w += blockDim.x) {
+        bitmap[w] = 0u;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const int tiles = (job.candidates + kTileCandidates - 1) / kTileCandidates;
-        const int done = __hip_atomic_fetch_add(a.counters + job_index, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_tile = done == tiles - 1 ? 1 : 0;
-        if (last_tile) {
-            __hip_atomic_store(a.counters + job_index, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int e = threadIdx.x; e < tiles * kept_stride; e += blockDim.x) {
+        const uint64_t key = keys[e];
+        if (key == ~0ull) {
+            continue;
+        }
+        // Keys of each tile below `key`: a lower bound over its sorted run (padded with keys above every real one),
+        // by binary decomposition of the count, eight runs at a time so that their LDS reads overlap.
+        int rank = 0;
+        for (int t0 = 0; t0 < tiles; t0 += 8) {
+            int below[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                below[u] = 0;
+            }
+#pragma unroll
+            for (int step = kTileCandidates; step > 0; step >>= 1) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int next = below[u] + step;
+                    if (t0 + u < tiles && next <= kept_stride && keys[(t0 + u) * kept_stride + next - 1] < key) {
+                        below[u] = next;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                rank += below[u];
+            }
+        }
+        if (rank < a.budget) {
+            const uint32_t index = static_cast<uint32_t>(key & 0xFFFFFFFFull);
+            atomicOr(&bitmap[index >> 5], 1u << (index & 31));
         }
     }
     __syncthreads();
-    if (!last_tile) {
-        return;
+    for (int w = threadIdx.x; w < words; w += blockDim.x) {
+        uint32_t count = 0;
+        for (int v = 0; v < w; ++v) {
+            count += __builtin_popcount(bitmap[v]);
+        }
+        before[w] = count;
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __syncthreads();
+    for (int index = threadIdx.x; index < job.candidates; index += blockDim.x) {
+        const uint32_t word = bitmap[index >> 5];
+        const uint32_t bit = 1u << (index & 31);
+        if ((word & bit) != 0) {
+            const int position = static_cast<int>(before[index >> 5] + __builtin_popcount(word & (bit - 1)));
+            a.lists[job.list + 1 + position] = (index + 1) * a.geo.summary_keys;
+        }
+    }
+}
+
+// The merge by sorting, for jobs of many tiles (where each key's rank would take many searches): one thread per pair
+// of padded keys (64 to 1,024), the kept keys bitonic-sorted in LDS; the first `budget` are the selected pages,
+// their indices sorted again in the same space (budget <= kept keys) give the list in ascending page order.
+constexpr int kSortThreads = 1024;
+constexpr int kSearchTiles = 16;  // jobs of more tiles take select_sort_kernel
+
+__global__ __launch_bounds__(kSortThreads) void select_sort_kernel(SelectArgs a) {
+    extern __shared__ __align__(16) uint8_t scratch[];
+    const SelectJob job = a.jobs[blockIdx.x];
     const int tiles = (job.candidates + kTileCandidates - 1) / kTileCandidates;
+    const int kept_stride = min(a.budget, kTileCandidates);
+    const uint64_t* job_keys = a.keys + static_cast<size_t>(blockIdx.x) * a.key_stride;
     uint64_t* merged_keys = reinterpret_cast<uint64_t*>(scratch);
     int merged = 0;
     for (int t = 0; t < tiles; ++t) {
@@ -277,9 +355,6 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
         }
         merged += kept;
     }
-    // Sorted by rank key (the array padded to a power of two with keys above every real one), the first `budget`
-    // keys are the selected pages; their indices, sorted again in the same space (budget <= merged), give the list
-    // in ascending page order (KvPageSelector marks pages; the list is read in key order).
     const int padded = next_power_of_two(merged);
     for (int entry = merged + threadIdx.x; entry < padded; entry += blockDim.x) {
         merged_keys[entry] = ~0ull;
@@ -293,7 +368,7 @@ __global__ __launch_bounds__(512) void select_kernel(SelectArgs a) {
     __syncthreads();
     bitonic_sort(merged_keys, chosen);
     for (int r = threadIdx.x; r < a.budget; r += blockDim.x) {
-        a.lists[job.list + 1 + r] = (static_cast<int32_t>(merged_keys[r]) + 1) * g.summary_keys;
+        a.lists[job.list + 1 + r] = (static_cast<int32_t>(merged_keys[r]) + 1) * a.geo.summary_keys;
     }
 }
 
@@ -320,16 +395,8 @@ hipError_t launch_select(const Launch& launch, const SelectArgs& args, int most_
     const dim3 grid(tiles > args.geo.kv_heads ? tiles : args.geo.kv_heads, args.summary_count + args.job_count);
     const dim3 block(kTileCandidates * args.geo.group);
     const int merged = tiles * (args.budget < kTileCandidates ? args.budget : kTileCandidates);
-#ifdef PROBE_PRINT
-    {
-        static int calls = 0;
-        if (calls++ % 97 == 0) {
-            fprintf(stderr, "select grid %u x %u block %u summaries %d jobs %d most %d merged %d\n", grid.x, grid.y,
-                    block.x, args.summary_count, args.job_count, most_candidates, merged);
-        }
-    }
-#endif
-    // Dynamic LDS may exceed the 64 KiB default (an FP32 tile at head_dim 128 takes 66,560 bytes).
+    // Dynamic LDS may exceed the 64 KiB default (an FP32 tile at head_dim 128 takes 66,560 bytes; the merge of
+    // 8,192 kept keys 64 KiB).
     static const hipError_t configured = [] {
         constexpr int kMostDynamic = 96 * 1024;
         hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel<_Float16>),
@@ -338,17 +405,39 @@ hipError_t launch_select(const Launch& launch, const SelectArgs& args, int most_
             status = hipFuncSetAttribute(reinterpret_cast<const void*>(select_kernel<float>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, kMostDynamic);
         }
+        if (status == hipSuccess) {
+            status = hipFuncSetAttribute(reinterpret_cast<const void*>(select_merge_kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kMostDynamic);
+        }
+        if (status == hipSuccess) {
+            status = hipFuncSetAttribute(reinterpret_cast<const void*>(select_sort_kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kMostDynamic);
+        }
         return status;
     }();
     if (configured != hipSuccess) {
         return configured;
     }
+    // Profile mode brackets both launches: the start event with the first, the stop event with the second.
+    const Launch first{launch.stream, launch.start, args.job_count > 0 ? nullptr : launch.stop};
     if (fp16) {
-        const size_t shared = select_shared_bytes<_Float16>(args.geo.head_dim, merged);
-        SYNAPSE_KV_LAUNCH_SHARED(select_kernel<_Float16>, grid, block, shared, launch, args);
+        SYNAPSE_KV_LAUNCH_SHARED(select_kernel<_Float16>, grid, block, select_shared_bytes<_Float16>(args.geo.head_dim),
+                                 first, args);
     } else {
-        const size_t shared = select_shared_bytes<float>(args.geo.head_dim, merged);
-        SYNAPSE_KV_LAUNCH_SHARED(select_kernel<float>, grid, block, shared, launch, args);
+        SYNAPSE_KV_LAUNCH_SHARED(select_kernel<float>, grid, block, select_shared_bytes<float>(args.geo.head_dim),
+                                 first, args);
+    }
+    if (args.job_count > 0) {
+        const Launch second{launch.stream, nullptr, launch.stop};
+        if (tiles <= kSearchTiles) {
+            const size_t shared = static_cast<size_t>(merged) * sizeof(uint64_t);
+            SYNAPSE_KV_LAUNCH_SHARED(select_merge_kernel, dim3(args.job_count), dim3(kMergeThreads), shared, second,
+                                     args);
+        } else {
+            const size_t shared = static_cast<size_t>(next_power_of_two(merged)) * sizeof(uint64_t);
+            const int threads = std::min(kSortThreads, std::max(64, next_power_of_two(merged) / 2));
+            SYNAPSE_KV_LAUNCH_SHARED(select_sort_kernel, dim3(args.job_count), dim3(threads), shared, second, args);
+        }
     }
     return hipGetLastError();
 }

@@ -317,3 +317,28 @@ def test_small_page_folds_through_page_ends_and_truncation(torch_gpu, activation
     for position in range(382, 400):
         pair.run([(0, position)], rng, expect_sparse=True)
     pair.check_contents(0)
+
+
+@pytest.mark.parametrize("activation_page,budget", [(16, 70), (16, 5), (32, 300)])
+def test_many_candidates_take_the_sort(torch_gpu, activation_page, budget):
+    """Rows of more than 1,024 candidate pages (16-position pages over an 18,000-position slot: 1,108 candidates;
+    32-position pages over 40,000: 1,235), whose per-job merge sorts the kept keys instead of ranking each by binary
+    searches, next to a short row that takes the search (both merges run in one step: the step's largest job picks
+    the kernel)."""
+    say("page activation many candidates", activation_page, budget)
+    length = 18000 if activation_page == 16 else 40000
+    pair = PagePair(torch_gpu, page=256, growth=1024, max_positions=length + 2048, slots=2,
+                    max_pages=2 * ((length + 2048) // 256) + 8, step_tokens=1024)
+    rng = np.random.default_rng(60 + activation_page + budget)
+    for slot, count in ((0, length), (1, 3000)):
+        for first in range(0, count, 1024):
+            tokens = [(slot, p) for p in range(first, min(count, first + 1024))]
+            assert pair.cpu.step(tokens) == 0
+            pair.gpu.step(tokens)
+            for layer in range(pair.layers):
+                rows = rng.standard_normal((len(tokens), pair.width)).astype(np.float32)
+                pair.gpu.append_rope(layer, torch_gpu.from_numpy(rows.copy()).cuda())
+                assert pair.cpu.append_rope(layer, rows, pair.cos, pair.sin) == 0
+    pair.activate(budget, 64, page_tokens=activation_page)
+    pair.run([(0, length), (1, 3000)], rng, expect_sparse=True)
+    pair.run([(0, length + 1), (1, 3001)], rng, fused=True, expect_sparse=True)
