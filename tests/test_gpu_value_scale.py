@@ -109,9 +109,9 @@ def test_shared_prefix_decode_with_scaled_values(torch_gpu):
 
 
 def test_prefill_over_a_long_cache_with_scaled_values(torch_gpu):
-    """A 256-token chunk over 4,096 cached tokens whose values are scaled too: past the first keys, most 64-key
-    steps hold a small share of each row's weight, which is where the prefill kernel drops the low parts of the
-    probabilities (the step's weights are then the FP16 high parts in numerator and row sum alike)."""
+    """A 256-token chunk over 4,096 cached tokens whose values are scaled too: past the first keys most 64-key
+    steps hold a small share of each row's weight, so an error of the probabilities would average over many keys
+    here, unlike the fresh prompt above; both must meet the bar."""
     torch = torch_gpu
     rng = np.random.default_rng(SEED + 3)
     cached, chunk = 4096, 256
