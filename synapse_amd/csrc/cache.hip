@@ -640,7 +640,7 @@ int64_t choose_prefill_chunk(const SynapseKvCache& cache, const SynapseKvBatchTo
     return best_chunk;
 }
 
-// Rank keys one key-bound selection job keeps between its tiles and its last tile.
+// Rank keys one key-bound selection job keeps between its tiles and its merge.
 size_t select_key_stride(const SynapseKvCache& cache, int32_t most_candidates) {
     const size_t tiles = (static_cast<size_t>(most_candidates) + 63) / 64;
     return tiles * std::min<size_t>(cache.activation.budget_pages, 64);
