@@ -31,36 +31,48 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the HIP library cannot be built")
 
 
+def _filter(text: str) -> str:
+    # the host pass does not know the device feature
+    return "\n".join(line for line in text.splitlines() if "packed-fp32-ops" not in line)
+
+
 def build_library(verbose: bool = False) -> Path:
+    """Compiles every csrc/*.hip to an object in parallel, then links the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
     OUTPUT.parent.mkdir(parents=True, exist_ok=True)
+    objects_dir = OUTPUT.parent / "obj"
+    objects_dir.mkdir(exist_ok=True)
+    flags = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", *DEVICE_FLAGS]
+
+    def compile_one(source: Path) -> tuple[Path, subprocess.CompletedProcess]:
+        target = objects_dir / (source.stem + ".o")
+        command = [hipcc(), *flags, "-c", "-o", str(target), str(source)]
+        return target, subprocess.run(command, cwd=PACKAGE, capture_output=True, text=True)
+
+    workers = max(1, min(len(SOURCES), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        results = list(pool.map(compile_one, SOURCES))
+    messages = []
+    for (target, result), source in zip(results, SOURCES):
+        output = _filter(result.stdout + result.stderr)
+        if result.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {source.name} ({result.returncode}):\n{output}")
+        if output.strip():
+            messages.append(output)
     temporary = OUTPUT.with_suffix(".so.tmp")
-    command = [
-        hipcc(),
-        f"--offload-arch={ARCH}",
-        "-O3",
-        "-std=c++17",
-        "-fPIC",
-        "-shared",
-        "-Wall",
-        "-Wno-unused-result",
-        # Every symbol resolved at link time: a kernel whose host launch stub the compiler did not emit fails the
-        # build here instead of the library's first load.
-        "-Wl,--no-undefined",
-        *DEVICE_FLAGS,
-        "-o",
-        str(temporary),
-        *map(str, SOURCES),
-    ]
+    # Every symbol resolved at link time: a kernel whose host launch stub the compiler did not emit fails the build
+    # here instead of the library's first load.
+    command = [hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-Wl,--no-undefined", "-o", str(temporary),
+               *(str(target) for target, _ in results)]
     result = subprocess.run(command, cwd=PACKAGE, capture_output=True, text=True)
-    output = "\n".join(
-        line
-        for line in (result.stdout + result.stderr).splitlines()
-        if "packed-fp32-ops" not in line  # the host pass does not know the device feature
-    )
+    output = _filter(result.stdout + result.stderr)
     if result.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({result.returncode}):\n{output}")
-    if verbose and output.strip():
-        print(output, file=sys.stderr)
+        raise RuntimeError(f"link failed ({result.returncode}):\n{output}")
+    if output.strip():
+        messages.append(output)
+    if verbose and messages:
+        print("\n".join(messages), file=sys.stderr)
     temporary.replace(OUTPUT)
     return OUTPUT
 

@@ -1,11 +1,12 @@
-// Q8_0 projections (QKV before the attention path, o_proj after it) on bf16 MFMA with exact products.
+// Q8_0 and K-quant projections (QKV before the attention path, o_proj after it, the feed-forward and logits of the
+// decoder step) on the matrix cores: bf16 with exact products for prompt runs, FP16 over a two-part input for decode.
 //
 // Semantics: synapse_q8_matvec_{1,2,4,8} and synapse_q8_gemm (native/synapse-gpu/src/Features/GpuKernels/cuda/
 // kernels/matmul.cu:1-189, metal/shaders/matmul.metal:1-310): output[t][out_column + row] = (accumulate ? output : 0)
 // + sum_blocks d * sum_k code[row][k] * input[t][k] + bias[row], rows of up to three matrices in one dispatch
 // (locate_segment, common.metal:138-146). Weights stay Q8_0, activations FP32, sums FP32 (ADR-012).
 //
-// Exact products on the bf16 matrix cores: each FP32 input x is split into three bf16 parts with
+// Prompt runs, exact products on the bf16 matrix cores: each FP32 input x is split into three bf16 parts with
 // x = hi + mid + lo exactly (bf16 keeps FP32's exponent range; each part takes the next 8 significant bits, and the
 // residuals x - hi and (x - hi) - mid are exact FP32 subtractions). A Q8_0 code is exact in bf16, and code * part
 // is a product of at most 8 by 8 significant bits, exact in FP32. One Q8_0 block (32 columns) is one k-depth of
@@ -14,8 +15,10 @@
 // matmul.cu:101-104). Only the order of the FP32 additions differs from the reference's kernels.
 //
 // MI355X mapping, decode (at most 16 tokens): project_decode_kernel, one workgroup per eight 16-row tiles and one
-// slice of at most eight 64-column chunks; the workgroup splits its input slice into LDS once and every wave streams
-// its tile's codes and scales against it (see below); reduce_kernel adds the slices in order with bias and residual.
+// slice of at most eight 64-column chunks; the workgroup splits its input slice into LDS once, as two FP16 parts of
+// the input scaled per token by a power of two (products exact in FP32; the parts hold the input to 2^-22), and every
+// wave streams its tile's codes and scales against it on v_mfma_f32_16x16x32_f16 (see below); reduce_kernel adds the
+// slices in order with bias and residual.
 //
 // K-quant matrices (Q4_K, Q6_K; kquant_layout.h) run the same kernels specialised on the encoding: a block's codes
 // are exact in bf16 too (0..15, -32..31), and its factors (a factor byte times an FP16 multiplier, exact in FP32)
@@ -311,25 +314,13 @@ __device__ inline void multiply_chunk(const ChunkWeights<E>& w, const InputFragm
 
 // A workgroup of eight waves covers eight 16-row tiles (one per wave; tiles of different matrices may meet in one
 // workgroup) over one slice of at most kDecodeSliceChunks column chunks. The workgroup first splits its slice of the
-// input into the three bf16 parts, in B-fragment order, into LDS; then every wave streams its tile's codes and
-// scales for the slice (its only vector-memory loads, all issued up front) and multiplies against the fragments in
-// LDS. Each slice's 16 x 16 sums go to partial rows; reduce_kernel adds the slices in order with the bias and the
-// residual. The input is read from L2 once per workgroup instead of once per tile. Eight waves share one 48 KiB
-// staged input (four did before: 16 resident waves per CU instead of 12; 3 % faster decoder steps). Streaming two
-// or four tiles per wave instead changed nothing measurable.
+// input into two FP16 parts (scaled per token by a power of two), in B-fragment order, into LDS; then every wave
+// streams its tile's codes and scales for the slice (its only vector-memory loads, all issued up front) and
+// multiplies against the fragments in LDS. Each slice's 16 x 16 sums go to partial rows; reduce_kernel adds the
+// slices in order with the bias and the residual. The input is read from L2 once per workgroup instead of once per
+// tile. Eight waves share one 32 KiB staged input, so four workgroups fit a CU's LDS.
 constexpr int kDecodeSliceChunks = 8;
 constexpr int kDecodeWaves = 8;
-
-// Row tiles per wave of the decode kernel (each wave would stream this many tiles' codes and factors against the
-// same staged input).
-template <uint32_t E>
-constexpr int decode_tiles_per_wave() {
-    return 1;
-}
-template <uint32_t E>
-constexpr int decode_tiles() {
-    return kDecodeWaves * decode_tiles_per_wave<E>();
-}
 
 __device__ inline int locate_tile(const ProjectionArgs& a, int tile, ProjectionSegment& seg) {
     int s = 0;
@@ -584,11 +575,260 @@ __global__ __launch_bounds__(kGemmWaves * 64, E == kEncodingQ6K ? 3 : 2) void pr
     }
 }
 
+// ---- Decode products on FP16 matrix cores: two input parts, scaled per token ---------------------------------
+
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx2 __attribute__((ext_vector_type(2)));
+constexpr int kDecodeParts = 2;
+
+// Four int8 codes (a little-endian word) as exact FP16 values, into elements at .. at + 3 of `out`: each biased
+// byte b = code + 128 becomes the FP16 bits 0x64bb = 1024 + b (one v_perm per pair), and one packed FP16
+// subtraction of 1152 per pair leaves the code (an integer of at most 8 bits: exact).
+__device__ inline void codes_to_half(uint32_t word, uint32_t bias_xor, _Float16 subtract, halfx8& out, int at) {
+    const uint32_t biased = word ^ bias_xor;
+    const uint32_t low = __builtin_amdgcn_perm(0x64646464u, biased, 0x04010400u);
+    const uint32_t high = __builtin_amdgcn_perm(0x64646464u, biased, 0x04030402u);
+    const halfx2 first = __builtin_bit_cast(halfx2, low) - halfx2{subtract, subtract};
+    const halfx2 second = __builtin_bit_cast(halfx2, high) - halfx2{subtract, subtract};
+    out[at] = first[0];
+    out[at + 1] = first[1];
+    out[at + 2] = second[0];
+    out[at + 3] = second[1];
+}
+
+// The chunk's two blocks of A fragments in FP16: Q8_0 / Q6_K int8 codes, Q4_K nibbles (block 0 low, block 1 high).
+template <uint32_t E>
+__device__ inline void weight_fragments_f16(uintx4 codes, halfx8 (&weight)[2]) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            if constexpr (E == kEncodingQ4K) {
+                codes_to_half((codes[w] >> (4 * b)) & 0x0F0F0F0Fu, 0u, static_cast<_Float16>(1024.0f), weight[b],
+                              4 * w);
+            } else {
+                codes_to_half(codes[2 * b + w], 0x80808080u, static_cast<_Float16>(1152.0f), weight[b], 4 * w);
+            }
+        }
+    }
+}
+
+// One chunk of the decode kernel: as multiply_chunk, with the input as two FP16 parts (x' = hi + lo to 2^-22 of
+// |x'|, x' the token's input scaled by a power of two) and FP16 codes. Each block's two part products go to a fresh
+// accumulator; the block sums are then scaled into the running sums in the reference's block order.
+template <uint32_t E, bool kWide = false>
+__device__ inline void multiply_chunk_f16(const ChunkWeights<E>& w, const halfx8 (&input)[2][kDecodeParts],
+                                          const float (&xsum)[2], floatx4& acc) {
+    halfx8 weight[2];
+    weight_fragments_f16<E>(w.codes, weight);
+    if constexpr (E == kEncodingQ8_0) {
+        uint32_t words[4];
+        if constexpr (kWide) {
+            words[0] = w.scales[0];
+            words[1] = w.scales[1];
+            words[2] = w.scales[2];
+            words[3] = w.scales[3];
+        } else {
+            const int bits = static_cast<int>(w.factor);
+            words[0] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, bits, 0x150, 0xF, 0xF, false));
+            words[1] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, bits, 0x151, 0xF, 0xF, false));
+            words[2] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, bits, 0x152, 0xF, 0xF, false));
+            words[3] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, bits, 0x153, 0xF, 0xF, false));
+        }
+        floatx4 block[2];
+#pragma unroll
+        for (int p = kDecodeParts - 1; p >= 0; --p) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                block[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    weight[b], input[b][p], p == kDecodeParts - 1 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : block[b], 0, 0,
+                    0);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const halfx2 pair = __builtin_bit_cast(halfx2, words[2 * b + h]);
+                acc[2 * h] = __builtin_fmaf(block[b][2 * h], static_cast<float>(pair[0]), acc[2 * h]);
+                acc[2 * h + 1] = __builtin_fmaf(block[b][2 * h + 1], static_cast<float>(pair[1]), acc[2 * h + 1]);
+            }
+        }
+    } else if constexpr (E == kEncodingQ4K) {
+        floatx4 block[2];
+#pragma unroll
+        for (int p = kDecodeParts - 1; p >= 0; --p) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                block[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    weight[b], input[b][p], p == kDecodeParts - 1 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : block[b], 0, 0,
+                    0);
+            }
+        }
+        float factors[16];
+        row_broadcast_factors(kquant_factor_bits(w), factors);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[i] = __builtin_fmaf(block[b][i], factors[b * 4 + i], acc[i]);
+                acc[i] = __builtin_fmaf(-factors[8 + b * 4 + i], xsum[b], acc[i]);
+            }
+        }
+    } else {
+        const bool first_half = (threadIdx.x & 63) < 32;  // lane groups 0 and 1: columns 0-15 of the block
+        const halfx8 zero = halfx8{};
+        halfx8 halves[2][2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            halves[0][b] = first_half ? weight[b] : zero;
+            halves[1][b] = first_half ? zero : weight[b];
+        }
+        floatx4 block[2][2];
+#pragma unroll
+        for (int p = kDecodeParts - 1; p >= 0; --p) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    block[h][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        halves[h][b], input[b][p],
+                        p == kDecodeParts - 1 ? floatx4{0.0f, 0.0f, 0.0f, 0.0f} : block[h][b], 0, 0, 0);
+                }
+            }
+        }
+        float factors[16];
+        row_broadcast_factors(kquant_factor_bits(w), factors);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[i] = __builtin_fmaf(block[h][b][i], factors[h * 8 + b * 4 + i], acc[i]);
+                }
+            }
+        }
+    }
+}
+
+// One row tile's codes and factors for a decode slice (a launch over both K-quant types keeps Q6_K-shaped registers
+// and notes whether the tile is Q4_K; a Q4_K tile fills only the first half of each code vector).
+template <uint32_t E>
+struct DecodeTile {
+    static constexpr uint32_t kStored = E == kEncodingMixedK ? kEncodingQ6K : E;
+    ChunkWeights<kStored> w[kDecodeSliceChunks];
+    bool q4k;
+};
+
+// Issues the loads of `tile`'s chunks k0 .. k0 + count - 1 (chunks past count re-read the last).
+template <uint32_t E>
+__device__ inline void load_decode_tile(const ProjectionArgs& a, int tile, int k0, int count, int lane, int g,
+                                        DecodeTile<E>& out) {
+    ProjectionSegment seg;
+    const int local = locate_tile(a, tile, seg);
+    const size_t first_chunk = static_cast<size_t>(local) * a.chunks + k0;
+    out.q4k = E == kEncodingQ4K || (E == kEncodingMixedK && seg.encoding == kEncodingQ4K);
+    if constexpr (E == kEncodingMixedK) {
+        if (out.q4k) {
+#pragma unroll
+            for (int i = 0; i < kDecodeSliceChunks; ++i) {
+                const ChunkWeights<kEncodingQ4K> w =
+                    load_chunk<kEncodingQ4K>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
+                out.w[i].codes = w.codes;
+                out.w[i].factor = w.factor;
+                out.w[i].multiplier = w.multiplier;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kDecodeSliceChunks; ++i) {
+                out.w[i] = load_chunk<kEncodingQ6K>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kDecodeSliceChunks; ++i) {
+            out.w[i] = load_chunk<E, true>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
+        }
+    }
+}
+
+// Multiplies a loaded tile against the staged slice and writes its 16 x 16 slice sums: lane (g, t) holds rows
+// 4 g .. + 3 of token t, partial[slice][t][16 * tile + 4 g + i], scaled back by the token's power of two (exact
+// barring underflow; every lane's token t = lane % 16 is the token whose scale `shift` this lane holds).
+template <uint32_t E>
+__device__ inline void multiply_decode_tile(const ProjectionArgs& a, const DecodeTile<E>& tile, int tile_index,
+                                            int slice, int count, const halfx8* staged, const float* group_sums,
+                                            int shift, int lane, int g) {
+    constexpr bool kSums = E == kEncodingQ4K || E == kEncodingMixedK;
+    floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < kDecodeSliceChunks; ++i) {
+        if (i < count) {
+            halfx8 input[2][kDecodeParts];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                for (int p = 0; p < kDecodeParts; ++p) {
+                    input[b][p] = staged[((i * kDecodeParts + p) * 2 + b) * 64 + lane];
+                }
+            }
+            float xsum[2] = {};
+            if constexpr (kSums) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const float* four = group_sums + (i * 8 + 4 * b) * 16 + (lane & 15);
+                    xsum[b] = ((four[0] + four[16]) + four[32]) + four[48];
+                }
+            }
+            if constexpr (E == kEncodingMixedK) {
+                if (tile.q4k) {
+                    ChunkWeights<kEncodingQ4K> w;
+                    w.codes = tile.w[i].codes;
+                    w.factor = tile.w[i].factor;
+                    w.multiplier = tile.w[i].multiplier;
+                    multiply_chunk_f16<kEncodingQ4K>(w, input, xsum, acc);
+                } else {
+                    multiply_chunk_f16<kEncodingQ6K>(tile.w[i], input, xsum, acc);
+                }
+            } else {
+                multiply_chunk_f16<E, true>(tile.w[i], input, xsum, acc);
+            }
+        }
+    }
+    const int t = lane & 15;
+    float* destination = a.partials + (static_cast<size_t>(slice) * 16 + t) * a.partial_stride +
+                         static_cast<size_t>(tile_index) * kQ8TileRows + 4 * g;
+    floatx4 value;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        value[i] = __builtin_ldexpf(acc[i], -shift);
+    }
+    *reinterpret_cast<floatx4*>(destination) = value;
+}
+
+// Decode kernel (at most 16 tokens). Each workgroup covers eight 16-row tiles (one per wave) over one slice of at
+// most eight 64-column chunks:
+//   1. every thread loads its inputs (token, 8 columns), then its wave's codes and factors for the slice (the wave's
+//      only other vector-memory loads, all in flight while the input is split);
+//   2. the workgroup finds each token's largest |x| over the slice and scales the token's inputs by the power of two
+//      that puts it in [2^14, 2^15) (exact; FP16 keeps every part of the scaled input in its normal range down to
+//      2^-18 of that largest value);
+//   3. each input is split into two FP16 parts, hi = fp16(x') and lo = fp16(x' - hi), in B-fragment order in LDS;
+//   4. every wave multiplies its tile's chunks against the staged parts on v_mfma_f32_16x16x32_f16 (FP16 codes and
+//      FP16 parts: products exact in FP32), and writes its 16 x 16 slice sums, scaled back by the power of two, to
+//      the partial rows that reduce_kernel (or the consuming norm / SwiGLU kernel) adds in slice order.
+// The products differ from FP32 x * FP32 code by the lo part's rounding, at most 2^-22 of |x| (FP32 products round
+// at 2^-24): well inside the accumulation error of any FP32 order of the sums. Against the three-part bf16 split
+// this takes two MFMAs per block instead of three, 1.25 VALU instructions per code instead of 1.5 and 32 KiB of
+// LDS instead of 48. A variant streaming several tiles per wave through two register sets (so the next tile's
+// loads overlap the current tile's products) measured slower: its registers allow one workgroup per CU instead of
+// four, and the one-shot workgroups already keep more bytes in flight.
 template <uint32_t E>
 __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(ProjectionArgs a) {
     constexpr int kItems = kDecodeSliceChunks * 128 / (kDecodeWaves * 64);  // split items per thread
-    constexpr int TW = decode_tiles_per_wave<E>();
-    __shared__ bf16x8 staged[kDecodeSliceChunks * kParts * 2 * 64];
+    __shared__ halfx8 staged[kDecodeSliceChunks * kDecodeParts * 2 * 64];
+    __shared__ float wave_maxima[kDecodeWaves][16];
     // Q4_K: per chunk, 8-column group and token, the sum of the 8 inputs.
     constexpr bool kSums = E == kEncodingQ4K || E == kEncodingMixedK;
     __shared__ float group_sums[kSums ? kDecodeSliceChunks * 8 * 16 : 1];
@@ -599,10 +839,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;
-    const int first_tile = (blockIdx.x * kDecodeWaves + wave) * TW;  // this wave's tiles: first_tile + k, k < TW
+    const int tile = blockIdx.x * kDecodeWaves + wave;  // this wave's row tile (past the last: loads the last)
 
-    // 1. This thread's input loads for the split: item = threadIdx.x + 256 j is (token item % 16, 8-column group
-    //    item / 16 of the slice). Tokens past the last and columns past the matrix read nothing (zeros).
+    // 1. This thread's input loads for the split: item = threadIdx.x + 512 j is (token item % 16, 8-column group
+    //    item / 16 of the slice); every item of a thread has token threadIdx.x % 16. Tokens past the last and
+    //    columns past the matrix read nothing (zeros).
     floatx4 raw[kItems][2];
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
@@ -620,46 +861,35 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
             raw[j][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
-    // 2. This wave's codes and scales for the slice, issued after the input loads: loads complete in issue order,
+    //    This wave's codes and factors for the slice, issued after the input loads: loads complete in issue order,
     //    so the split below waits for the input only, while the weight stream stays in flight.
-    //    A tile past the last loads the last tile again.
-    //    A launch over both K-quant types (kEncodingMixedK) keeps Q6_K-shaped registers and branches per wave on its
-    //    tile's segment (uniform per wave); a Q4_K tile fills only the first half of each code vector.
-    constexpr uint32_t kStored = E == kEncodingMixedK ? kEncodingQ6K : E;
-    ChunkWeights<kStored> batch[TW][kDecodeSliceChunks];
-    bool q4k_tile[TW];
+    DecodeTile<E> weights;
+    load_decode_tile<E>(a, min(tile, a.total_tiles - 1), k0, count, lane, g, weights);
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. The token's largest |x| over the slice: this thread's items, the wave's four lanes of the token
+    //    (lanes t, t + 16, t + 32, t + 48), then the eight waves through LDS.
+    float largest = 0.0f;
 #pragma unroll
-    for (int k = 0; k < TW; ++k) {
-        ProjectionSegment seg;
-        const int tile = locate_tile(a, min(first_tile + k, a.total_tiles - 1), seg);
-        const size_t first_chunk = static_cast<size_t>(tile) * a.chunks + k0;
-        q4k_tile[k] = E == kEncodingQ4K || (E == kEncodingMixedK && seg.encoding == kEncodingQ4K);
-        if constexpr (E == kEncodingMixedK) {
-            if (q4k_tile[k]) {
+    for (int j = 0; j < kItems; ++j) {
 #pragma unroll
-                for (int i = 0; i < kDecodeSliceChunks; ++i) {
-                    const ChunkWeights<kEncodingQ4K> w =
-                        load_chunk<kEncodingQ4K>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
-                    batch[k][i].codes = w.codes;
-                    batch[k][i].factor = w.factor;
-                    batch[k][i].multiplier = w.multiplier;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < kDecodeSliceChunks; ++i) {
-                    batch[k][i] = load_chunk<kEncodingQ6K>(seg.codes, seg.scales, first_chunk + min(i, count - 1),
-                                                           lane, g);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < kDecodeSliceChunks; ++i) {
-                batch[k][i] = load_chunk<E, true>(seg.codes, seg.scales, first_chunk + min(i, count - 1), lane, g);
-            }
+        for (int i = 0; i < 8; ++i) {
+            largest = fmaxf(largest, fabsf(raw[j][i / 4][i % 4]));
         }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // 3. Split into the three bf16 parts, in B-fragment order, into LDS.
+    largest = fmaxf(largest, __shfl_xor(largest, 16));
+    largest = fmaxf(largest, __shfl_xor(largest, 32));
+    if (lane < 16) {
+        wave_maxima[wave][lane] = largest;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) {
+        largest = fmaxf(largest, wave_maxima[w][lane & 15]);
+    }
+    int exponent = 0;
+    (void)frexpf(largest, &exponent);  // largest = m 2^exponent, m in [0.5, 1) (0 for a zero slice)
+    const int shift = 15 - exponent;
+    // 3. Split into the two FP16 parts, in B-fragment order, into LDS.
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
         const int item = threadIdx.x + j * kDecodeWaves * 64;
@@ -669,20 +899,18 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
         const int within = 8 * (group & 7);  // column within the chunk
         const int block = within / kQ8BlockElements;
         const int lane_group = (within % kQ8BlockElements) / 8;
-        bf16x8 parts[kParts];
+        halfx8 parts[kDecodeParts];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            __bf16 hi;
-            __bf16 mid;
-            __bf16 lo;
-            split3(raw[j][i / 4][i % 4], hi, mid, lo);
+#pragma clang fp contract(off)
+            const float x = __builtin_ldexpf(raw[j][i / 4][i % 4], shift);
+            const _Float16 hi = static_cast<_Float16>(x);
             parts[0][i] = hi;
-            parts[1][i] = mid;
-            parts[2][i] = lo;
+            parts[1][i] = static_cast<_Float16>(x - static_cast<float>(hi));
         }
 #pragma unroll
-        for (int p = 0; p < kParts; ++p) {
-            staged[((chunk * kParts + p) * 2 + block) * 64 + 16 * lane_group + t] = parts[p];
+        for (int p = 0; p < kDecodeParts; ++p) {
+            staged[((chunk * kDecodeParts + p) * 2 + block) * 64 + 16 * lane_group + t] = parts[p];
         }
         if constexpr (kSums) {
             float sum = raw[j][0][0];
@@ -690,63 +918,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
             for (int i = 1; i < 8; ++i) {
                 sum += raw[j][i / 4][i % 4];
             }
-            group_sums[(chunk * 8 + (group & 7)) * 16 + t] = sum;
+            // Scaled like the parts, so the offset term matches the scaled products (exact: a power of two).
+            group_sums[(chunk * 8 + (group & 7)) * 16 + t] = __builtin_ldexpf(sum, shift);
         }
     }
     __syncthreads();
 
-    // 4. Multiply the slice against the staged input.
-    floatx4 acc[TW][1];
-#pragma unroll
-    for (int k = 0; k < TW; ++k) {
-        acc[k][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-#pragma unroll
-    for (int i = 0; i < kDecodeSliceChunks; ++i) {
-        if (i < count) {
-            InputFragments<1> input;
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-#pragma unroll
-                for (int p = 0; p < kParts; ++p) {
-                    input.x[0][b][p] = staged[((i * kParts + p) * 2 + b) * 64 + lane];
-                }
-            }
-            float xsum[1][2] = {};
-            if constexpr (kSums) {
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const float* four = group_sums + (i * 8 + 4 * b) * 16 + (lane & 15);
-                    xsum[0][b] = ((four[0] + four[16]) + four[32]) + four[48];
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < TW; ++k) {
-                if constexpr (E == kEncodingMixedK) {
-                    if (q4k_tile[k]) {
-                        ChunkWeights<kEncodingQ4K> w;
-                        w.codes = batch[k][i].codes;
-                        w.factor = batch[k][i].factor;
-                        w.multiplier = batch[k][i].multiplier;
-                        multiply_chunk<kEncodingQ4K, 1>(w, input, xsum, acc[k]);
-                    } else {
-                        multiply_chunk<kEncodingQ6K, 1>(batch[k][i], input, xsum, acc[k]);
-                    }
-                } else {
-                    multiply_chunk<E, 1, true>(batch[k][i], input, xsum, acc[k]);
-                }
-            }
-        }
-    }
-    // Lane (g, t) holds rows 4 g .. + 3 of token t: partial[slice][t][16 * tile + 4 g + i].
-    const int t = lane & 15;
-#pragma unroll
-    for (int k = 0; k < TW; ++k) {
-        if (first_tile + k < a.total_tiles) {
-            float* destination = a.partials + (static_cast<size_t>(slice) * 16 + t) * a.partial_stride +
-                                 static_cast<size_t>(first_tile + k) * kQ8TileRows + 4 * g;
-            *reinterpret_cast<floatx4*>(destination) = acc[k][0];
-        }
+    // 4. Multiply and write the slice sums.
+    if (tile < a.total_tiles) {
+        multiply_decode_tile<E>(a, weights, tile, slice, count, staged, group_sums, shift, lane, g);
     }
 }
 
@@ -828,27 +1008,19 @@ hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, i
     const Launch plain{launch.stream, nullptr, nullptr};
     if (args.tokens <= 16) {
         const dim3 block(kDecodeWaves * 64);
+        const dim3 grid((tiles + kDecodeWaves - 1) / kDecodeWaves, args.slices);
         switch (args.encoding) {
             case kEncodingQ4K:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ4K>,
-                                  dim3((tiles + decode_tiles<kEncodingQ4K>() - 1) / decode_tiles<kEncodingQ4K>(), args.slices),
-                                  block, launch, args);
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ4K>, grid, block, launch, args);
                 break;
             case kEncodingQ6K:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ6K>,
-                                  dim3((tiles + decode_tiles<kEncodingQ6K>() - 1) / decode_tiles<kEncodingQ6K>(), args.slices),
-                                  block, launch, args);
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ6K>, grid, block, launch, args);
                 break;
             case kEncodingMixedK:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingMixedK>,
-                                  dim3((tiles + decode_tiles<kEncodingMixedK>() - 1) / decode_tiles<kEncodingMixedK>(),
-                                       args.slices),
-                                  block, launch, args);
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingMixedK>, grid, block, launch, args);
                 break;
             default:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ8_0>,
-                                  dim3((tiles + decode_tiles<kEncodingQ8_0>() - 1) / decode_tiles<kEncodingQ8_0>(), args.slices),
-                                  block, launch, args);
+                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ8_0>, grid, block, launch, args);
                 break;
         }
         if (reduce) {

@@ -2,7 +2,7 @@
 file and tokens.
 
 Bar (the reference's Metal-vs-reference bar, MetalBackendTests.cs:60): max |gpu - oracle| <= 0.002 x the range of
-the oracle's logits, per step. The GPU sums in other orders (MFMA projections over a bf16 split of the inputs,
+the oracle's logits, per step. The GPU sums in other orders (MFMA projections over an FP16 or bf16 split of the inputs,
 split-K attention); the oracle follows the reference kernels' FP32 order. Both KV precisions; FP16 KV rounds K and V
 to nearest even on both sides.
 """
