@@ -2,8 +2,8 @@
 
 Projections: against an FP64 product with the exactly decoded weights (projection.dequantize; the decoders are
 pinned by tests/test_oracle_kquant.py). Bar: |gpu - fp64| <= 2^-18 * sum_k (|scale * q| + |offset|) * |x_k|
-(+ |bias|, + |old output| when accumulating): the kernels multiply exact products (codes and the bf16 split of x
-on the matrix cores) and apply each block's FP32 factors to its sum, as the reference's factored form
+(+ |bias|, + |old output| when accumulating): the kernels multiply codes by a split of x on the matrix cores
+(prompt runs: three bf16 parts, exact; decode: two FP16 parts of x scaled per token, x to 2^-22) and apply each block's FP32 factors to its sum, as the reference's factored form
 scale * dot(q, x) - offset * sum(x) does (matmul_kquant.metal:115-119), in another FP32 order. A wrong nibble, a
 swapped half-block scale or a dropped offset moves outputs by far more (about 1e-2 of that sum).
 

@@ -1,8 +1,9 @@
 """Q8_0 projections on the GPU through the C ABI, against the FP64 restatement on the same seeded inputs.
 
 Bar: |gpu - fp64| <= 2^-18 * sum_k |d * code * x| (+ |bias|, + |old output| when accumulating) per element: FP32
-summation of the exact products in another order (the reference's own FP32 matrix-vector order stays within
-2^-20 of the anchor, tests/test_oracle_projection.py). A dropped or mis-scaled 32-column block moves an output by
+summation in another order of products that are exact (prompt runs: three bf16 parts of x) or within 2^-22 of
+exact (decode: two FP16 parts of x scaled per token); the reference's own FP32 matrix-vector order stays within
+2^-20 of the anchor, tests/test_oracle_projection.py. A dropped or mis-scaled 32-column block moves an output by
 about 1e-3 of that sum at these widths. Weights read back from the device are bit-exact with the uploaded blocks.
 """
 
