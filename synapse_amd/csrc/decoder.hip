@@ -332,6 +332,7 @@ struct SynapseKvDecoder {
     synapse_kv::Buffer<float> norms;        // per layer [attention norm | feed-forward norm], then the output norm
     synapse_kv::Buffer<float> hidden;       // [step_tokens][hidden]: the residual stream
     synapse_kv::Buffer<float> normalized;   // [step_tokens][hidden]
+    synapse_kv::Buffer<float> squares;      // decode steps: [16][kNormSquaresStride] partial sums of squares of hidden
     synapse_kv::Buffer<float> qkv;          // [step_tokens][hidden + 2 kv_width]
     synapse_kv::Buffer<float> attention;    // [step_tokens][hidden]
     synapse_kv::Buffer<float> gate_up;      // [step_tokens][2 feed_forward]
@@ -349,8 +350,8 @@ struct SynapseKvDecoder {
         }
         synapse_kv_cache_destroy(cache);
         synapse_kv_weights_destroy(weights);
-        for (auto* buffer : {&hidden, &normalized, &qkv, &attention, &gate_up, &feed_forward, &logits_input, &logits,
-                             &norms}) {
+        for (auto* buffer : {&hidden, &normalized, &squares, &qkv, &attention, &gate_up, &feed_forward, &logits_input,
+                             &logits, &norms}) {
             buffer->reset();
         }
         embedding.reset();
@@ -535,6 +536,8 @@ void create_decoder(const SynapseKvDecoderDesc& d, int32_t device, SynapseKvDeco
     const size_t steps = d.step_tokens;
     model->hidden.allocate(steps * d.hidden, "hidden rows");
     model->normalized.allocate(steps * d.hidden, "normalized rows");
+    model->squares.allocate(16 * kNormSquaresStride, "row squares");
+    check_hip(hipMemset(model->squares.pointer, 0, 16 * kNormSquaresStride * sizeof(float)), "row squares");
     model->qkv.allocate(steps * (d.hidden + 2 * kv), "qkv rows");
     model->attention.allocate(steps * d.hidden, "attention rows");
     model->gate_up.allocate(steps * 2 * static_cast<size_t>(d.feed_forward), "gate/up rows");
@@ -687,6 +690,15 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
             break;
     }
     check_hip(hipGetLastError(), "embedding");
+    // Decode steps (at most 16 tokens) fold the attention norms into the QKV projection's staging: the embedding and
+    // each down projection's reduce leave the hidden rows' partial sums of squares (NormInput).
+    const bool decode = n <= 16;
+    const int32_t norm_parts = static_cast<int32_t>((hidden + kNormSquaresColumns - 1) / kNormSquaresColumns);
+    if (decode) {
+        check_hip(launch_row_squares(m.stream, m.hidden.pointer, static_cast<int>(hidden), static_cast<int>(n),
+                                     m.squares.pointer),
+                  "row squares");
+    }
     // Prompt steps (more than 16 tokens) have the norms and SwiGLU write the next projection's split input
     // directly (three launches fewer per layer); SYNAPSE_KV_OPTION_FUSED_SUMS = 0 keeps FP32 rows and split_kernel.
     // Both give the same bits.
@@ -703,6 +715,17 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
                                attention_norm, hidden, d.rms_epsilon, split);
             check_hip(hipGetLastError(), "attention norm");
             project_split(*m.weights, p, split, m.qkv.pointer);
+        } else if (decode) {
+            NormInput norm;
+            norm.weight = attention_norm;
+            norm.squares = m.squares.pointer;
+            norm.parts = norm_parts;
+            norm.columns = static_cast<int32_t>(hidden);
+            norm.epsilon = d.rms_epsilon;
+            project_normalized(*m.weights,
+                               projection({{base, 0}, {base + 1, hidden}, {base + 2, hidden + kv}}, n, hidden,
+                                          qkv_width, false),
+                               m.hidden.pointer, m.qkv.pointer, norm);
         } else {
             hipLaunchKernelGGL(rms_norm_kernel, dim3(n), dim3(kNormThreads), 0, m.stream, m.hidden.pointer,
                                static_cast<const int32_t*>(nullptr), attention_norm, hidden, d.rms_epsilon,
@@ -766,7 +789,12 @@ void forward(SynapseKvDecoder& m, const SynapseKvBatchToken* tokens, size_t coun
         check_hip(hipGetLastError(), "SwiGLU");
         // The down projection's slice sums (a slice per 512 columns of 18,944: 37 at the 7B shape) are added by its
         // own reduce: one workgroup per token reading them all in the next norm measured slower than the launch.
-        project(m, {{base + 6, 0}}, n, m.feed_forward.pointer, ffn, m.hidden.pointer, hidden, true);
+        if (decode) {
+            project_with_squares(*m.weights, projection({{base + 6, 0}}, n, ffn, hidden, true), m.feed_forward.pointer,
+                                 m.hidden.pointer, m.squares.pointer);
+        } else {
+            project(m, {{base + 6, 0}}, n, m.feed_forward.pointer, ffn, m.hidden.pointer, hidden, true);
+        }
     }
     if (rows > 0) {
         const float* output_norm = m.norms.pointer + static_cast<size_t>(2 * d.layer_count) * hidden;

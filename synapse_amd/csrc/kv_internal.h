@@ -178,6 +178,21 @@ struct ProjectionSegment {
     uint32_t encoding;  // GGML type of this segment's matrix
 };
 
+// A decode projection whose input is an RMS-normalized row (synapse_rms_norm, elementwise.cu:17-52): the kernel reads
+// the raw row and normalizes it while staging, y = x * (1 / sqrt(total / columns + epsilon)) * weight, with total
+// the in-order sum of the token's `parts` partial sums of squares (squares[token * kNormSquaresStride + part], part
+// j covering columns 256 j .. 256 j + 255), written by the kernel that produced the row.
+constexpr int kNormSquaresStride = 32;  // rows of up to 8,192 columns
+constexpr int kNormSquaresColumns = 256;
+struct NormInput {
+    const float* weight = nullptr;  // null: the input is used as it is
+    const float* squares = nullptr;
+    int32_t parts = 0;
+    int32_t columns = 0;
+    float epsilon = 0.0f;
+    int32_t pad = 0;
+};
+
 struct ProjectionArgs {
     ProjectionSegment segment[3];
     int32_t segments;
@@ -199,6 +214,8 @@ struct ProjectionArgs {
                              // take kEncodingMixedK: K-quant segments of both types (each segment's own field)
     int32_t pad;
     float* sums;             // prompt runs of Q4_K: [tokens][padded_columns / 8] sums of 8 inputs (scratch)
+    NormInput norm;          // decode: normalize the input rows while staging (norm.weight non-null)
+    float* squares;          // decode with reduce: also write the output rows' partial sums of squares (NormInput)
 };
 
 // KV page activation (ADR-016). Key summaries live in their own buffer, one summary page per pool page:
@@ -457,6 +474,16 @@ namespace synapse_kv {
 bool cache_fused_sums(const SynapseKvCache& cache);
 DeferredSums project_deferred(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input,
                               float* output);
+// Decode projections (at most 16 tokens) around the decoder's RMS norms. project_normalized projects the rows of
+// `input` normalized per `norm` (the norm kernel's launch folded into the projection's staging);
+// project_with_squares adds the projection into `output` (accumulate) and writes, per token, the partial sums of
+// squares of the output row that a later project_normalized reads (one segment, no other output columns).
+void project_normalized(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output,
+                        const NormInput& norm);
+void project_with_squares(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output,
+                          float* squares);
+// Partial sums of squares of `tokens` rows of `columns` floats (row stride `columns`) into squares.
+hipError_t launch_row_squares(hipStream_t stream, const float* rows, int columns, int tokens, float* squares);
 // A prompt run (more than 16 tokens) whose input the caller writes already split: prepare_split returns the
 // weights' scratch sized for the projection (sums included when a matrix is Q4_K), valid until the next projection
 // on the weights' stream; project_split runs the projection from it. Work queued on the weights' stream may be

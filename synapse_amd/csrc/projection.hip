@@ -753,13 +753,11 @@ __device__ inline void load_decode_tile(const ProjectionArgs& a, int tile, int k
     }
 }
 
-// Multiplies a loaded tile against the staged slice and writes its 16 x 16 slice sums: lane (g, t) holds rows
-// 4 g .. + 3 of token t, partial[slice][t][16 * tile + 4 g + i], scaled back by the token's power of two (exact
-// barring underflow; every lane's token t = lane % 16 is the token whose scale `shift` this lane holds).
+// Multiplies a loaded tile against the staged slice: lane (g, t) returns rows 4 g .. + 3 of token t, in the scaled
+// input's units.
 template <uint32_t E>
-__device__ inline void multiply_decode_tile(const ProjectionArgs& a, const DecodeTile<E>& tile, int tile_index,
-                                            int slice, int count, const halfx8* staged, const float* group_sums,
-                                            int shift, int lane, int g) {
+__device__ inline floatx4 multiply_decode_tile(const DecodeTile<E>& tile, int count, const halfx8* staged,
+                                               const float* group_sums, int lane) {
     constexpr bool kSums = E == kEncodingQ4K || E == kEncodingMixedK;
     floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -796,6 +794,13 @@ __device__ inline void multiply_decode_tile(const ProjectionArgs& a, const Decod
             }
         }
     }
+    return acc;
+}
+
+// Writes a tile's 16 x 16 slice sums: partial[slice][t][16 * tile + 4 g + i], scaled back by the token's power of two
+// (exact barring underflow; every lane's token t = lane % 16 is the token whose scale `shift` this lane holds).
+__device__ inline void store_tile_sums(const ProjectionArgs& a, floatx4 acc, int tile_index, int slice, int shift,
+                                       int lane, int g) {
     const int t = lane & 15;
     float* destination = a.partials + (static_cast<size_t>(slice) * 16 + t) * a.partial_stride +
                          static_cast<size_t>(tile_index) * kQ8TileRows + 4 * g;
@@ -807,46 +812,23 @@ __device__ inline void multiply_decode_tile(const ProjectionArgs& a, const Decod
     *reinterpret_cast<floatx4*>(destination) = value;
 }
 
-// Decode kernel (at most 16 tokens). Each workgroup covers eight 16-row tiles (one per wave) over one slice of at
-// most eight 64-column chunks:
-//   1. every thread loads its inputs (token, 8 columns), then its wave's codes and factors for the slice (the wave's
-//      only other vector-memory loads, all in flight while the input is split);
-//   2. the workgroup finds each token's largest |x| over the slice and scales the token's inputs by the power of two
-//      that puts it in [2^14, 2^15) (exact; FP16 keeps every part of the scaled input in its normal range down to
-//      2^-18 of that largest value);
-//   3. each input is split into two FP16 parts, hi = fp16(x') and lo = fp16(x' - hi), in B-fragment order in LDS;
-//   4. every wave multiplies its tile's chunks against the staged parts on v_mfma_f32_16x16x32_f16 (FP16 codes and
-//      FP16 parts: products exact in FP32), and writes its 16 x 16 slice sums, scaled back by the power of two, to
-//      the partial rows that reduce_kernel (or the consuming norm / SwiGLU kernel) adds in slice order.
-// The products differ from FP32 x * FP32 code by the lo part's rounding, at most 2^-22 of |x| (FP32 products round
-// at 2^-24): well inside the accumulation error of any FP32 order of the sums. Against the three-part bf16 split
-// this takes two MFMAs per block instead of three, 1.25 VALU instructions per code instead of 1.5 and 32 KiB of
-// LDS instead of 48. A variant streaming several tiles per wave through two register sets (so the next tile's
-// loads overlap the current tile's products) measured slower: its registers allow one workgroup per CU instead of
-// four, and the one-shot workgroups already keep more bytes in flight.
-template <uint32_t E>
-__global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(ProjectionArgs a) {
-    constexpr int kItems = kDecodeSliceChunks * 128 / (kDecodeWaves * 64);  // split items per thread
-    __shared__ halfx8 staged[kDecodeSliceChunks * kDecodeParts * 2 * 64];
-    __shared__ float wave_maxima[kDecodeWaves][16];
-    // Q4_K: per chunk, 8-column group and token, the sum of the 8 inputs.
-    constexpr bool kSums = E == kEncodingQ4K || E == kEncodingMixedK;
-    __shared__ float group_sums[kSums ? kDecodeSliceChunks * 8 * 16 : 1];
-    const int slice = blockIdx.y;
-    const int k0 = slice * a.chunks / a.slices;
-    const int k1 = (slice + 1) * a.chunks / a.slices;
-    const int count = k1 - k0;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;
-    const int tile = blockIdx.x * kDecodeWaves + wave;  // this wave's row tile (past the last: loads the last)
+// Input loads of a decode slice: item = threadIdx.x + 512 j is (token item % 16, 8-column group item / 16 of the
+// slice); every item of a thread has token threadIdx.x % 16. Tokens past the last and columns past the matrix read
+// nothing (zeros). With NORM the thread also loads the norm weights of its columns and its token's partial sums of
+// squares.
+constexpr int kDecodeItems = kDecodeSliceChunks * 128 / (kDecodeWaves * 64);  // split items per thread
 
-    // 1. This thread's input loads for the split: item = threadIdx.x + 512 j is (token item % 16, 8-column group
-    //    item / 16 of the slice); every item of a thread has token threadIdx.x % 16. Tokens past the last and
-    //    columns past the matrix read nothing (zeros).
-    floatx4 raw[kItems][2];
+template <bool NORM>
+struct SliceInput {
+    floatx4 raw[kDecodeItems][2];
+    floatx4 weight[NORM ? kDecodeItems : 1][2];
+    floatx4 squares[NORM ? kNormSquaresStride / 4 : 1];
+};
+
+template <bool NORM>
+__device__ inline void load_slice_input(const ProjectionArgs& a, int k0, int count, SliceInput<NORM>& in) {
 #pragma unroll
-    for (int j = 0; j < kItems; ++j) {
+    for (int j = 0; j < kDecodeItems; ++j) {
         const int item = threadIdx.x + j * kDecodeWaves * 64;
         const int t = item & 15;
         const int group = item >> 4;
@@ -854,23 +836,76 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
         const bool inside = (group >> 3) < count && t < a.tokens && column < a.columns;
         const floatx4* source = reinterpret_cast<const floatx4*>(
             a.input + static_cast<size_t>(inside ? t : 0) * a.in_stride + (inside ? column : 0));
-        raw[j][0] = source[0];
-        raw[j][1] = source[1];
+        in.raw[j][0] = source[0];
+        in.raw[j][1] = source[1];
         if (!inside) {
-            raw[j][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-            raw[j][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            in.raw[j][0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            in.raw[j][1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if constexpr (NORM) {
+            const floatx4* weight = reinterpret_cast<const floatx4*>(a.norm.weight + (inside ? column : 0));
+            in.weight[j][0] = weight[0];
+            in.weight[j][1] = weight[1];
         }
     }
-    //    This wave's codes and factors for the slice, issued after the input loads: loads complete in issue order,
-    //    so the split below waits for the input only, while the weight stream stays in flight.
-    DecodeTile<E> weights;
-    load_decode_tile<E>(a, min(tile, a.total_tiles - 1), k0, count, lane, g, weights);
-    __builtin_amdgcn_sched_barrier(0);
-    // 2. The token's largest |x| over the slice: this thread's items, the wave's four lanes of the token
-    //    (lanes t, t + 16, t + 32, t + 48), then the eight waves through LDS.
+    if constexpr (NORM) {
+        const int t = min(static_cast<int>(threadIdx.x & 15), a.tokens - 1);
+        const floatx4* squares = reinterpret_cast<const floatx4*>(a.norm.squares + t * kNormSquaresStride);
+#pragma unroll
+        for (int i = 0; i < kNormSquaresStride / 4; ++i) {
+            in.squares[i] = 4 * i < a.norm.parts ? squares[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+}
+
+// y = x * (1 / sqrt(total / columns + epsilon)) * w (normalize_values' arithmetic, decoder.hip), total the in-order
+// sum of the token's partial sums of squares.
+template <bool NORM>
+__device__ inline void normalize_slice_input(const ProjectionArgs& a, SliceInput<NORM>& in) {
+    if constexpr (NORM) {
+#pragma clang fp contract(off)
+        float total = in.squares[0][0];
+#pragma unroll
+        for (int i = 1; i < kNormSquaresStride; ++i) {
+            if (i < a.norm.parts) {
+                total += in.squares[i / 4][i % 4];
+            }
+        }
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(a.norm.columns) + a.norm.epsilon);
+#pragma unroll
+        for (int j = 0; j < kDecodeItems; ++j) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    in.raw[j][h][e] = in.raw[j][h][e] * scale * in.weight[j][h][e];
+                }
+            }
+        }
+    }
+}
+
+// LDS of a decode workgroup: the staged input parts, the waves' per-token maxima and (Q4_K) the input sums.
+template <uint32_t E>
+struct DecodeShared {
+    static constexpr bool kSums = E == kEncodingQ4K || E == kEncodingMixedK;
+    halfx8 staged[kDecodeSliceChunks * kDecodeParts * 2 * 64];
+    float wave_maxima[kDecodeWaves][16];
+    float group_sums[kSums ? kDecodeSliceChunks * 8 * 16 : 1];  // per chunk, 8-column group and token
+};
+
+// Stages the slice (the loaded `raw` inputs) and returns the token's power-of-two shift:
+//   1. each token's largest |x| over the slice: this thread's items, the wave's four lanes of the token (lanes t,
+//      t + 16, t + 32, t + 48), then the eight waves through LDS; the shift puts it in [2^14, 2^15) (exact; FP16 then
+//      keeps every part of the scaled input in its normal range down to 2^-18 of that largest value);
+//   2. each input is split into two FP16 parts, hi = fp16(x') and lo = fp16(x' - hi), in B-fragment order in LDS
+//      (Q4_K: and the scaled sums of 8 inputs).
+template <uint32_t E>
+__device__ inline int stage_slice(const floatx4 (&raw)[kDecodeItems][2], DecodeShared<E>& shared, int wave,
+                                  int lane) {
     float largest = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kItems; ++j) {
+    for (int j = 0; j < kDecodeItems; ++j) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             largest = fmaxf(largest, fabsf(raw[j][i / 4][i % 4]));
@@ -879,19 +914,18 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
     largest = fmaxf(largest, __shfl_xor(largest, 16));
     largest = fmaxf(largest, __shfl_xor(largest, 32));
     if (lane < 16) {
-        wave_maxima[wave][lane] = largest;
+        shared.wave_maxima[wave][lane] = largest;
     }
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < kDecodeWaves; ++w) {
-        largest = fmaxf(largest, wave_maxima[w][lane & 15]);
+        largest = fmaxf(largest, shared.wave_maxima[w][lane & 15]);
     }
     int exponent = 0;
     (void)frexpf(largest, &exponent);  // largest = m 2^exponent, m in [0.5, 1) (0 for a zero slice)
     const int shift = 15 - exponent;
-    // 3. Split into the two FP16 parts, in B-fragment order, into LDS.
 #pragma unroll
-    for (int j = 0; j < kItems; ++j) {
+    for (int j = 0; j < kDecodeItems; ++j) {
         const int item = threadIdx.x + j * kDecodeWaves * 64;
         const int t = item & 15;
         const int group = item >> 4;
@@ -910,23 +944,69 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(Proje
         }
 #pragma unroll
         for (int p = 0; p < kDecodeParts; ++p) {
-            staged[((chunk * kDecodeParts + p) * 2 + block) * 64 + 16 * lane_group + t] = parts[p];
+            shared.staged[((chunk * kDecodeParts + p) * 2 + block) * 64 + 16 * lane_group + t] = parts[p];
         }
-        if constexpr (kSums) {
+        if constexpr (DecodeShared<E>::kSums) {
             float sum = raw[j][0][0];
 #pragma unroll
             for (int i = 1; i < 8; ++i) {
                 sum += raw[j][i / 4][i % 4];
             }
             // Scaled like the parts, so the offset term matches the scaled products (exact: a power of two).
-            group_sums[(chunk * 8 + (group & 7)) * 16 + t] = __builtin_ldexpf(sum, shift);
+            shared.group_sums[(chunk * 8 + (group & 7)) * 16 + t] = __builtin_ldexpf(sum, shift);
         }
     }
     __syncthreads();
+    return shift;
+}
 
-    // 4. Multiply and write the slice sums.
+// Decode kernel (at most 16 tokens). Each workgroup covers eight 16-row tiles (one per wave) over one slice of at
+// most eight 64-column chunks:
+//   1. every thread loads its inputs (token, 8 columns), then its wave's codes and factors for the slice (the wave's
+//      only other vector-memory loads, all in flight while the input is split);
+//   2. the workgroup finds each token's largest |x| over the slice and scales the token's inputs by the power of two
+//      that puts it in [2^14, 2^15) (exact; FP16 keeps every part of the scaled input in its normal range down to
+//      2^-18 of that largest value);
+//   3. each input is split into two FP16 parts, hi = fp16(x') and lo = fp16(x' - hi), in B-fragment order in LDS;
+//   4. every wave multiplies its tile's chunks against the staged parts on v_mfma_f32_16x16x32_f16 (FP16 codes and
+//      FP16 parts: products exact in FP32), and writes its 16 x 16 slice sums, scaled back by the power of two, to
+//      the partial rows that reduce_kernel (or the consuming norm / SwiGLU kernel) adds in slice order.
+// The products differ from FP32 x * FP32 code by the lo part's rounding, at most 2^-22 of |x| (FP32 products round
+// at 2^-24): well inside the accumulation error of any FP32 order of the sums. Against the three-part bf16 split
+// this takes two MFMAs per block instead of three, 1.25 VALU instructions per code instead of 1.5 and 32 KiB of
+// LDS instead of 48 (decoder step 5.67 -> 5.59 ms for Q8_0, 6.00 -> 5.79-5.86 for Q4_K_M).
+// With NORM the input is a raw row that the kernel RMS-normalizes while staging (NormInput), in place of the norm
+// kernel's launch and its normalized copy of the rows.
+// A variant streaming 2-8 tiles per wave through two register sets (the next tile's loads in flight while the
+// current one is multiplied; loads past a wave's last tile through empty-range buffer resources so the waits stay
+// partial; sums stored after the last tile) measured slower: gate + up 38.3 against 34.2 us, logits 135.5 against
+// 127.5. Its 182 VGPRs allow one workgroup per CU where the one-shot kernel runs two to four. With the multiplies
+// skipped the one-shot kernel's loads alone take 26.2 us on gate + up (5.5 TB/s) and 89 us on the logits: the
+// multiplies cost a quarter of the launch that they do not overlap. Occupancy (three, four or five waves per SIMD
+// through launch bounds or compact scales) changed nothing measurable.
+template <uint32_t E, bool NORM>
+__global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(ProjectionArgs a) {
+    __shared__ DecodeShared<E> shared;
+    const int slice = blockIdx.y;
+    const int k0 = slice * a.chunks / a.slices;
+    const int count = (slice + 1) * a.chunks / a.slices - k0;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    const int tile = blockIdx.x * kDecodeWaves + wave;  // this wave's row tile (past the last: loads the last)
+
+    SliceInput<NORM> input;
+    load_slice_input<NORM>(a, k0, count, input);
+    // This wave's codes and factors for the slice, issued after the input loads: loads complete in issue order, so
+    // the staging waits for the input only, while the weight stream stays in flight.
+    DecodeTile<E> weights;
+    load_decode_tile<E>(a, min(tile, a.total_tiles - 1), k0, count, lane, g, weights);
+    __builtin_amdgcn_sched_barrier(0);
+    normalize_slice_input<NORM>(a, input);
+    const int shift = stage_slice<E>(input.raw, shared, wave, lane);
     if (tile < a.total_tiles) {
-        multiply_decode_tile<E>(a, weights, tile, slice, count, staged, group_sums, shift, lane, g);
+        store_tile_sums(a, multiply_decode_tile<E>(weights, count, shared.staged, shared.group_sums, lane), tile,
+                        slice, shift, lane, g);
     }
 }
 
@@ -970,7 +1050,88 @@ __global__ __launch_bounds__(256) void reduce_kernel(ProjectionArgs a) {
     *destination = a.accumulate != 0 ? *destination + total : total;
 }
 
+// The partial sum of squares of a workgroup's 256 values (one per thread, zeros past the row): each wave's 64 in a
+// fixed butterfly, then the four waves in order.
+__device__ inline float block_squares(float x) {
+    __shared__ float waves[4];
+    float square = x * x;
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        square += __shfl_xor(square, offset);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        waves[threadIdx.x >> 6] = square;
+    }
+    __syncthreads();
+    return ((waves[0] + waves[1]) + waves[2]) + waves[3];
+}
+
+// reduce_kernel for a one-segment decode projection whose output rows feed an RMS norm: workgroup (part, token)
+// writes output[t][out_column + row] for 256 rows exactly as reduce_kernel does, then the part's sum of squares of
+// the written values into squares[t * kNormSquaresStride + part].
+__global__ __launch_bounds__(256) void reduce_squares_kernel(ProjectionArgs a) {
+    const int t = blockIdx.y;
+    const int row = blockIdx.x * kNormSquaresColumns + threadIdx.x;
+    const ProjectionSegment& seg = a.segment[0];
+    float value = 0.0f;
+    if (row < seg.rows) {
+        const float* partial = a.partials + static_cast<size_t>(t) * a.partial_stride + row;
+        const size_t stride = static_cast<size_t>(16) * a.partial_stride;
+        float sum = partial[0];
+        int slice = 1;
+        for (; slice + 8 <= a.slices; slice += 8) {
+            float values[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                values[i] = partial[(slice + i) * stride];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                sum += values[i];
+            }
+        }
+        for (; slice < a.slices; ++slice) {
+            sum += partial[slice * stride];
+        }
+        const float total = sum + (seg.bias != nullptr ? seg.bias[row] : 0.0f);
+        float* destination = a.output + static_cast<size_t>(t) * a.out_stride + seg.out_column + row;
+        value = a.accumulate != 0 ? *destination + total : total;
+        *destination = value;
+    }
+    const float squares = block_squares(value);
+    if (threadIdx.x == 0) {
+        a.squares[t * kNormSquaresStride + blockIdx.x] = squares;
+    }
+}
+
+// Partial sums of squares of rows another kernel wrote (the embedding), as reduce_squares_kernel writes them.
+__global__ __launch_bounds__(256) void row_squares_kernel(const float* rows, int columns, float* squares) {
+    const int t = blockIdx.y;
+    const int column = blockIdx.x * kNormSquaresColumns + threadIdx.x;
+    const float value = column < columns ? rows[static_cast<size_t>(t) * columns + column] : 0.0f;
+    const float sum = block_squares(value);
+    if (threadIdx.x == 0) {
+        squares[t * kNormSquaresStride + blockIdx.x] = sum;
+    }
+}
+
+template <uint32_t E>
+void launch_decode(const Launch& launch, const ProjectionArgs& args, int tiles) {
+    const dim3 grid((tiles + kDecodeWaves - 1) / kDecodeWaves, args.slices);
+    if (args.norm.weight != nullptr) {
+        SYNAPSE_KV_LAUNCH((project_decode_kernel<E, true>), grid, dim3(kDecodeWaves * 64), launch, args);
+    } else {
+        SYNAPSE_KV_LAUNCH((project_decode_kernel<E, false>), grid, dim3(kDecodeWaves * 64), launch, args);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_row_squares(hipStream_t stream, const float* rows, int columns, int tokens, float* squares) {
+    hipLaunchKernelGGL(row_squares_kernel, dim3((columns + kNormSquaresColumns - 1) / kNormSquaresColumns, tokens),
+                       dim3(256), 0, stream, rows, columns, squares);
+    return hipGetLastError();
+}
 
 int projection_decode_slices(int chunks) { return (chunks + kDecodeSliceChunks - 1) / kDecodeSliceChunks; }
 
@@ -1007,23 +1168,24 @@ hipError_t launch_gemm(const Launch& launch, const ProjectionArgs& args, int til
 hipError_t launch_projection(const Launch& launch, const ProjectionArgs& args, int tiles, bool reduce, bool split) {
     const Launch plain{launch.stream, nullptr, nullptr};
     if (args.tokens <= 16) {
-        const dim3 block(kDecodeWaves * 64);
-        const dim3 grid((tiles + kDecodeWaves - 1) / kDecodeWaves, args.slices);
         switch (args.encoding) {
             case kEncodingQ4K:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ4K>, grid, block, launch, args);
+                launch_decode<kEncodingQ4K>(launch, args, tiles);
                 break;
             case kEncodingQ6K:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ6K>, grid, block, launch, args);
+                launch_decode<kEncodingQ6K>(launch, args, tiles);
                 break;
             case kEncodingMixedK:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingMixedK>, grid, block, launch, args);
+                launch_decode<kEncodingMixedK>(launch, args, tiles);
                 break;
             default:
-                SYNAPSE_KV_LAUNCH(project_decode_kernel<kEncodingQ8_0>, grid, block, launch, args);
+                launch_decode<kEncodingQ8_0>(launch, args, tiles);
                 break;
         }
-        if (reduce) {
+        if (reduce && args.squares != nullptr) {
+            const dim3 grid((args.segment[0].rows + kNormSquaresColumns - 1) / kNormSquaresColumns, args.tokens);
+            SYNAPSE_KV_LAUNCH(reduce_squares_kernel, grid, dim3(256), plain, args);
+        } else if (reduce) {
             const int outputs = args.tokens * tiles * kQ8TileRows;
             SYNAPSE_KV_LAUNCH(reduce_kernel, dim3((outputs + 255) / 256), dim3(256), plain, args);
         }

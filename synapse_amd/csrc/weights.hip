@@ -177,8 +177,13 @@ void ensure_scratch(SynapseKvWeights& weights, size_t needed) {
 // One launch over segments [first, first + count) of the projection, which share an encoding. With `presplit` (a
 // prompt run) the input is already split in the scratch and `input` is not read.
 DeferredSums launch_run(SynapseKvWeights& weights, const SynapseKvProjection& p, uint32_t first, uint32_t count,
-                        const float* input, float* output, bool reduce = true, const SplitInput* presplit = nullptr) {
+                        const float* input, float* output, bool reduce = true, const SplitInput* presplit = nullptr,
+                        const NormInput* norm = nullptr, float* squares = nullptr) {
     ProjectionArgs args{};
+    if (norm != nullptr) {
+        args.norm = *norm;
+    }
+    args.squares = squares;
     int tiles = 0;
     uint32_t columns = 0;
     for (uint32_t s = 0; s < count; ++s) {
@@ -285,7 +290,7 @@ void validate_projection(SynapseKvWeights& weights, const SynapseKvProjection& p
 // Consecutive segments of one encoding share a launch (the kernels are specialised per encoding); decode runs
 // (at most 16 tokens) also put Q4_K and Q6_K segments in one launch.
 void project_runs(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output,
-                  const SplitInput* presplit) {
+                  const SplitInput* presplit, const NormInput* norm = nullptr) {
     auto joins = [&](uint32_t a, uint32_t b) {
         const uint32_t x = weights.matrices[p.matrix[a]].encoding;
         const uint32_t y = weights.matrices[p.matrix[b]].encoding;
@@ -297,7 +302,7 @@ void project_runs(SynapseKvWeights& weights, const SynapseKvProjection& p, const
         while (first + count < p.segments && joins(first, first + count)) {
             ++count;
         }
-        launch_run(weights, p, first, count, input, output, true, presplit);
+        launch_run(weights, p, first, count, input, output, true, presplit, norm);
         first += count;
     }
 }
@@ -324,6 +329,28 @@ DeferredSums project_deferred(SynapseKvWeights& weights, const SynapseKvProjecti
         return DeferredSums{};
     }
     return launch_run(weights, p, 0, p.segments, input, output, false);
+}
+
+void project_normalized(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output,
+                        const NormInput& norm) {
+    validate_projection(weights, p, input, output);
+    if (p.tokens > 16 || norm.weight == nullptr || norm.squares == nullptr || norm.parts < 1 ||
+        norm.parts > kNormSquaresStride || norm.columns != static_cast<int32_t>(weights.matrices[p.matrix[0]].columns) ||
+        (norm.parts - 1) * kNormSquaresColumns >= norm.columns || norm.parts * kNormSquaresColumns < norm.columns) {
+        invalid("a normalized projection takes at most 16 tokens and the squares of its input columns");
+    }
+    project_runs(weights, p, input, output, nullptr, &norm);
+}
+
+void project_with_squares(SynapseKvWeights& weights, const SynapseKvProjection& p, const float* input, float* output,
+                          float* squares) {
+    validate_projection(weights, p, input, output);
+    const DeviceMatrix& m = weights.matrices[p.matrix[0]];
+    if (p.tokens > 16 || p.segments != 1 || squares == nullptr || p.out_column[0] != 0 || m.rows != p.out_stride ||
+        (m.rows + kNormSquaresColumns - 1) / kNormSquaresColumns > static_cast<uint32_t>(kNormSquaresStride)) {
+        invalid("a projection with squares takes at most 16 tokens and one matrix filling its output rows");
+    }
+    launch_run(weights, p, 0, 1, input, output, true, nullptr, nullptr, squares);
 }
 
 SplitInput prepare_split(SynapseKvWeights& weights, const SynapseKvProjection& p) {
