@@ -974,7 +974,7 @@ __device__ inline int stage_slice(const floatx4 (&raw)[kDecodeItems][2], DecodeS
 // The products differ from FP32 x * FP32 code by the lo part's rounding, at most 2^-22 of |x| (FP32 products round
 // at 2^-24): well inside the accumulation error of any FP32 order of the sums. Against the three-part bf16 split
 // this takes two MFMAs per block instead of three, 1.25 VALU instructions per code instead of 1.5 and 32 KiB of
-// LDS instead of 48 (decoder step 5.67 -> 5.59 ms for Q8_0, 6.00 -> 5.79-5.86 for Q4_K_M).
+// LDS instead of 48 (decoder step, same box: Q8_0 5.70 -> 5.69 ms, Q4_K_M 6.11 -> 5.88).
 // With NORM the input is a raw row that the kernel RMS-normalizes while staging (NormInput), in place of the norm
 // kernel's launch and its normalized copy of the rows.
 // A variant streaming 2-8 tiles per wave through two register sets (the next tile's loads in flight while the
@@ -982,8 +982,8 @@ __device__ inline int stage_slice(const floatx4 (&raw)[kDecodeItems][2], DecodeS
 // partial; sums stored after the last tile) measured slower: gate + up 38.3 against 34.2 us, logits 135.5 against
 // 127.5. Its 182 VGPRs allow one workgroup per CU where the one-shot kernel runs two to four. With the multiplies
 // skipped the one-shot kernel's loads alone take 26.2 us on gate + up (5.5 TB/s) and 89 us on the logits: the
-// multiplies cost a quarter of the launch that they do not overlap. Occupancy (three, four or five waves per SIMD
-// through launch bounds or compact scales) changed nothing measurable.
+// multiplies cost a quarter of the launch that they do not overlap. Compact Q8_0 scales (one register per chunk,
+// broadcast at use: 73 VGPRs instead of 95) measured the same.
 template <uint32_t E, bool NORM>
 __global__ __launch_bounds__(kDecodeWaves * 64) void project_decode_kernel(ProjectionArgs a) {
     __shared__ DecodeShared<E> shared;
