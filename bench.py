@@ -144,7 +144,8 @@ def measured_peaks(mfma: bool = False, read_bytes: int | None = None) -> dict:
     """
     from bench_support.calibrate import measure
 
-    result = measure(gib=2.0, repeats=5, mfma=mfma, read_sizes=(read_bytes,) if read_bytes else ())
+    result = measure(gib=2.0, repeats=5, mfma=mfma, read_sizes=(read_bytes,) if read_bytes else (),
+                     pattern_sizes=(read_bytes,) if read_bytes else ())
     out = {"read_gbps": result["read_gbps"], "copy_gbps": result["copy_gbps"],
            "source": "bench_support/calibrate.py: 2 GiB streaming read with 16-byte non-temporal loads (best of "
                      "8/16/32 waves per CU) and copy, measured in this run"}
@@ -156,6 +157,12 @@ def measured_peaks(mfma: bool = False, read_bytes: int | None = None) -> dict:
         (size, gbps), = result["read_gbps_at_bytes"].items()
         out["read_gbps_same_size"] = gbps
         out["same_size_bytes"] = size
+        if result.get("pattern_gbps_at_bytes"):
+            (size, gbps), = result["pattern_gbps_at_bytes"].items()
+            out["pattern_gbps_same_size"] = gbps
+            out["pattern_source"] = ("bench_support/calibrate.py pattern_kernel: the decode kernel's loads without its "
+                                     "arithmetic (one wave per SIMD, 32 KiB steps through two register sets), "
+                                     f"{size} bytes")
     return out
 
 
@@ -1131,6 +1138,8 @@ def main() -> None:
     result["roofline"]["measured_peak"] = peaks
     result["roofline"]["frac_of_measured_read"] = round(decode_gbps / peaks["read_gbps"], 4)
     result["roofline"]["frac_of_measured_read_same_size"] = round(decode_gbps / peaks["read_gbps_same_size"], 4)
+    if "pattern_gbps_same_size" in peaks:
+        result["roofline"]["frac_of_decode_pattern"] = round(decode_gbps / peaks["pattern_gbps_same_size"], 4)
     result["hbm_frac_of_measured_read"] = round(step_gbps / peaks["read_gbps"], 4)
     if not args.no_cpu_baseline and activation is None:
         threads = cpu_threads(args)

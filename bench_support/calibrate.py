@@ -2,6 +2,9 @@
 
 - read: 16-byte non-temporal loads over a large buffer, eight in flight per lane (bench_support/calibrate.hip);
   the practical ceiling of a streaming read, which the decode kernel is compared with beside the published 8 TB/s;
+- pattern: the decode kernel's access pattern without its arithmetic (one wave per SIMD, each streaming its own
+  run of 32 KiB steps through two register sets), over the decode launch's own byte count: the ceiling for that
+  kernel's structure at that size;
 - copy: the same with non-temporal stores (bytes read + written);
 - torch copy and torch sum (library kernels, for reference); the torch copy is also the reference kernel for
   scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters (its counters against the bytes it is known to move);
@@ -32,7 +35,10 @@ def load() -> ctypes.CDLL:
     library.calibrate_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                                        ctypes.c_void_p]
     library.calibrate_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    for function in (library.calibrate_read, library.calibrate_copy, library.calibrate_mfma):
+    library.calibrate_pattern.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                          ctypes.c_void_p]
+    for function in (library.calibrate_read, library.calibrate_copy, library.calibrate_mfma,
+                     library.calibrate_pattern):
         function.restype = ctypes.c_int
     return library
 
@@ -51,7 +57,8 @@ def _time(torch, stream, body, repeats: int) -> float:
     return start.elapsed_time(end) * 1e-3 / repeats
 
 
-def measure(gib: float = 4.0, repeats: int = 10, mfma: bool = True, read_sizes: tuple = ()) -> dict:
+def measure(gib: float = 4.0, repeats: int = 10, mfma: bool = True, read_sizes: tuple = (),
+            pattern_sizes: tuple = ()) -> dict:
     """Streaming read, copy and MFMA ceilings of this device.
 
     `read_sizes` adds the read rate over the first n bytes of the same buffer for each n (rounded down to
@@ -85,6 +92,14 @@ def measure(gib: float = 4.0, repeats: int = 10, mfma: bool = True, read_sizes: 
         best = min(_time(torch, stream, lambda: check(library.calibrate_read(
             source.data_ptr(), size, sink.data_ptr(), cus * per_cu, handle)), repeats * 4) for per_cu in (2, 4, 8))
         at_bytes[size] = round(size / best / 1e9, 1)
+    pattern = {}
+    for size in pattern_sizes:
+        steps = max(1, int(size) // (32768 * cus * 4))
+        moved = steps * 32768 * cus * 4
+        if moved <= nbytes:
+            seconds = _time(torch, stream, lambda: check(library.calibrate_pattern(
+                source.data_ptr(), steps, sink.data_ptr(), cus, handle)), repeats * 4)
+            pattern[moved] = round(moved / seconds / 1e9, 1)
     copy_s = _time(torch, stream, lambda: check(library.calibrate_copy(source.data_ptr(), target.data_ptr(), nbytes,
                                                                        blocks, handle)), repeats)
     torch_copy_s = _time(torch, stream, lambda: target.copy_(source), repeats)
@@ -101,6 +116,8 @@ def measure(gib: float = 4.0, repeats: int = 10, mfma: bool = True, read_sizes: 
     }
     if at_bytes:
         result["read_gbps_at_bytes"] = at_bytes
+    if pattern:
+        result["pattern_gbps_at_bytes"] = pattern
     if mfma:
         for wide, name in ((0, "16x16x32"), (1, "32x32x16")):
             for per_cu in (2, 4):
