@@ -121,32 +121,30 @@ __device__ inline float add_half_row(float value) {
                                                                          0xF, false));
 }
 
-// B operand of S^T = K Q^T for one lane (g, r): dims 32*ks + 8*g .. +7 of query head r % 8 of the group of
-// `kv_head` of `token`, rotated (when the call asks for RoPE) at the token's position. The FP32 query is split
-// exactly into FP16 parts q = hi + lo (hi = q rounded to FP16, lo = the remainder rounded to FP16; |q - hi - lo|
-// <= 2^-22 |q| for normal parts): columns 0..7 carry hi and columns 8..15 lo of the same heads (a GQA group has at
-// most 8 heads), so one MFMA gives both products and add_half_row joins them: the product of the FP16 keys with
-// the FP32 query to about FP32 accuracy, at no extra MFMA. Zero for columns past the group. With D/2 = 32 * (D/64)
-// the RoPE partner of dim i < D/2 (i + D/2) sits in the same lane at ks + D/64.
 template <int D>
-__device__ inline void load_query_f16(const AttentionArgs& a, int token, int position, int kv_head,
-                                      half8 (&query)[D / 32]) {
+struct QueryLoads {
+    float values[D / 32][8];
+    float cosines[D / 64][8];
+    float sines[D / 64][8];
+};
+
+template <int D>
+__device__ inline void issue_query_f16(const AttentionArgs& a, int token, int position, int kv_head,
+                                       QueryLoads<D>& loads) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;
     const int column = lane & 7;
-    const bool low_part = (lane & 8) != 0;
     const bool valid = column < a.geo.group;
     const float* q = a.qkv + static_cast<size_t>(token) * a.qkv_stride +
                      static_cast<size_t>(kv_head * a.geo.group + (valid ? column : 0)) * D;
-    float values[D / 32][8];
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
         const floatx4 lo = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g);
         const floatx4 hi = *reinterpret_cast<const floatx4*>(q + 32 * ks + 8 * g + 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            values[ks][j] = lo[j];
-            values[ks][j + 4] = hi[j];
+            loads.values[ks][j] = lo[j];
+            loads.values[ks][j + 4] = hi[j];
         }
     }
     if (a.rotate) {
@@ -157,8 +155,32 @@ __device__ inline void load_query_f16(const AttentionArgs& a, int token, int pos
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int i = 32 * ks + 8 * g + j;
-                rotate_pair(values[ks][j], values[ks + D / 64][j], cosines[i], sines[i], values[ks][j],
-                            values[ks + D / 64][j]);
+                loads.cosines[ks][j] = cosines[i];
+                loads.sines[ks][j] = sines[i];
+            }
+        }
+    }
+}
+
+// B operand of S^T = K Q^T for one lane (g, r): dims 32*ks + 8*g .. +7 of query head r % 8 of the group of
+// `kv_head` of `token`, rotated (when the call asks for RoPE) at the token's position. The FP32 query is split
+// exactly into FP16 parts q = hi + lo (hi = q rounded to FP16, lo = the remainder rounded to FP16; |q - hi - lo|
+// <= 2^-22 |q| for normal parts): columns 0..7 carry hi and columns 8..15 lo of the same heads (a GQA group has at
+// most 8 heads), so one MFMA gives both products and add_half_row joins them: the product of the FP16 keys with
+// the FP32 query to about FP32 accuracy, at no extra MFMA. Zero for columns past the group. With D/2 = 32 * (D/64)
+// the RoPE partner of dim i < D/2 (i + D/2) sits in the same lane at ks + D/64.
+template <int D>
+__device__ inline void finish_query_f16(const AttentionArgs& a, QueryLoads<D>& loads, half8 (&query)[D / 32]) {
+    const int lane = threadIdx.x & 63;
+    const bool low_part = (lane & 8) != 0;
+    const bool valid = (lane & 7) < a.geo.group;
+    if (a.rotate) {
+#pragma unroll
+        for (int ks = 0; ks < D / 64; ++ks) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                rotate_pair(loads.values[ks][j], loads.values[ks + D / 64][j], loads.cosines[ks][j],
+                            loads.sines[ks][j], loads.values[ks][j], loads.values[ks + D / 64][j]);
             }
         }
     }
@@ -166,23 +188,32 @@ __device__ inline void load_query_f16(const AttentionArgs& a, int token, int pos
     for (int ks = 0; ks < D / 32; ++ks) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float value = valid ? values[ks][j] : 0.0f;
+            const float value = valid ? loads.values[ks][j] : 0.0f;
             const _Float16 high = static_cast<_Float16>(value);
             query[ks][j] = low_part ? static_cast<_Float16>(value - static_cast<float>(high)) : high;
         }
     }
 }
 
+template <int D>
+__device__ inline void load_query_f16(const AttentionArgs& a, int token, int position, int kv_head,
+                                      half8 (&query)[D / 32]) {
+    QueryLoads<D> loads;
+    issue_query_f16<D>(a, token, position, kv_head, loads);
+    finish_query_f16<D>(a, loads, query);
+}
+
 // Loads the FP16 fragments of the 64-key block holding key0 (a multiple of 64) of one (slot table, KV head).
+// `known_page` >= 0: the block's pool page (from the plan), else read from the block table.
 template <int D>
 __device__ inline void fetch_f16(const Geometry& geo, const int32_t* table, size_t key_region, size_t value_region,
-                                 int key0, Fragments16<D>& fragments) {
+                                 int key0, Fragments16<D>& fragments, int known_page = -1) {
     const int lane = threadIdx.x & 63;
     const int logical = key0 / geo.page_tokens;
     const int within = key0 - logical * geo.page_tokens;
+    const int page_index = known_page >= 0 ? known_page : load_uniform(table + logical);
     const _Float16* page =
-        reinterpret_cast<const _Float16*>(geo.pool + static_cast<uint64_t>(load_uniform(table + logical)) *
-                                                       geo.page_bytes);
+        reinterpret_cast<const _Float16*>(geo.pool + static_cast<uint64_t>(page_index) * geo.page_bytes);
     // 64-key blocks in fragment order: every load below is one contiguous 1 KiB wave load.
     const half8* keys = reinterpret_cast<const half8*>(page + key_region + static_cast<size_t>(within) * D) + lane;
     const half8* values = reinterpret_cast<const half8*>(page + value_region + static_cast<size_t>(within) * D) + lane;
@@ -264,10 +295,11 @@ __device__ inline void step_f16(const Fragments16<D>& fragments, const half8 (&q
 // page of a.geo.summary_keys keys from key list[s] (the 64-key block holding it is read, its other keys masked); keys
 // at or past `key_limit` are masked. The list is read with uniform (scalar) loads. With PREFETCH the next step's
 // fragments are loaded before the current step is computed.
+// With PREFETCH the caller has already requested the first step's block into `first` (attend_f16).
 template <int D, bool PREFETCH>
 __device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, int kv_head, int step_begin,
                                   int step_end, const int32_t* list, int key_limit, const half8 (&query)[D / 32],
-                                  WaveState<D>& state) {
+                                  WaveState<D>& state, Fragments16<D>& first) {
     const Geometry& geo = a.geo;
     const size_t key_region = region_offset(geo, 0, kv_head);
     const size_t value_region = region_offset(geo, 1, kv_head);
@@ -293,12 +325,11 @@ __device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, 
         // runs while at least two steps remain, so both of its fetches are unconditional and every step waits only
         // for its own fragments (a fetch under a branch would leave the number of loads in flight unknown at the
         // join, and the step after it would wait for the prefetched block too); the last one or two steps follow.
-        Fragments16<D> even;
+        Fragments16<D>& even = first;
         Fragments16<D> odd;
         constexpr int kBlock = ~(kStepKeys - 1);
         int step = step_begin;
         int key0 = first_key(step);
-        fetch_f16<D>(geo, table, key_region, value_region, key0 & kBlock, even);
         while (step + 2 < step_end) {
             const int key1 = first_key(step + 1);
             const int key2 = first_key(step + 2);
@@ -321,16 +352,30 @@ __device__ void attend_blocks_f16(const AttentionArgs& a, const int32_t* table, 
 }
 
 // One token's segment for one KV head, FP16 pages.
+// With PREFETCH the segment's first K/V block is requested between the query's loads and its use (the query and
+// the block are one round trip, not two), from the plan's page of that block when it has one.
 template <int D, bool PREFETCH>
 __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
     const Geometry& geo = a.geo;
-    half8 query[D / 32];
-    load_query_f16<D>(a, seg.token, seg.position, seg.kv_head, query);
     const int32_t* table = geo.block_table + static_cast<size_t>(seg.slot) * geo.pages_per_slot;
     const int32_t* list = seg.list >= 0 ? a.lists + seg.list : nullptr;
-    attend_blocks_f16<D, PREFETCH>(a, table, seg.kv_head, seg.key_begin / kStepKeys,
-                                   (seg.key_end + kStepKeys - 1) / kStepKeys, list,
-                                   list != nullptr ? seg.position + 1 : seg.key_end, query, state);
+    const int step_begin = seg.key_begin / kStepKeys;
+    half8 query[D / 32];
+    Fragments16<D> first;
+    if constexpr (PREFETCH) {
+        QueryLoads<D> loads;
+        issue_query_f16<D>(a, seg.token, seg.position, seg.kv_head, loads);
+        __builtin_amdgcn_sched_barrier(0);
+        const int key0 = list != nullptr ? load_uniform(list + step_begin) : step_begin * kStepKeys;
+        fetch_f16<D>(geo, table, region_offset(geo, 0, seg.kv_head), region_offset(geo, 1, seg.kv_head),
+                     key0 & ~(kStepKeys - 1), first, list != nullptr ? -1 : seg.first_page);
+        __builtin_amdgcn_sched_barrier(0);
+        finish_query_f16<D>(a, loads, query);
+    } else {
+        load_query_f16<D>(a, seg.token, seg.position, seg.kv_head, query);
+    }
+    attend_blocks_f16<D, PREFETCH>(a, table, seg.kv_head, step_begin, (seg.key_end + kStepKeys - 1) / kStepKeys, list,
+                                   list != nullptr ? seg.position + 1 : seg.key_end, query, state, first);
 }
 
 // One token's segment for one KV head, FP32 pages.
@@ -391,9 +436,11 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
         const int key_end = list != nullptr ? min(entry + geo.summary_keys, key_limit) : key_limit;
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
-        const float* page =
-            reinterpret_cast<const float*>(geo.pool + static_cast<uint64_t>(load_uniform(table + logical)) *
-                                           geo.page_bytes);
+        // The first step's page comes with the plan (no table read before the wave's first request).
+        const int page_index =
+            step == seg.key_begin / kStepKeys && list == nullptr && seg.first_page >= 0 ? seg.first_page
+                                                                                       : load_uniform(table + logical);
+        const float* page = reinterpret_cast<const float*>(geo.pool + static_cast<uint64_t>(page_index) * geo.page_bytes);
         const floatx4* keys =
             reinterpret_cast<const floatx4*>(page + key_region + static_cast<size_t>(within) * D) + lane;
         const floatx4* values =
@@ -541,16 +588,19 @@ __device__ void append_row(const AttentionArgs& a, const DecodeSegment& seg) {
 
 template <int D, bool F16, bool PREFETCH>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
-    // The worker range and the segment descriptors are uniform reads of the step's plan (scalar loads): the
-    // descriptor carries everything a segment needs before its query and first block can be requested.
+    // The segment descriptors are uniform reads of the step's plan (scalar loads): a descriptor carries everything
+    // a segment needs before its query and first block can be requested, the block's pool page included.
     const int worker = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + (threadIdx.x >> 6));
     if (worker >= a.workers) {
         return;
     }
-    const int first = load_uniform(a.worker_segments + worker);
-    const int last = load_uniform(a.worker_segments + worker + 1);
-    for (int index = first; index < last; ++index) {
+    // Worker w's first segment is segment w; the later ones follow `next`.
+    for (int index = worker; index >= 0;) {
         const DecodeSegment seg = load_uniform(a.segments + index);
+        index = seg.next;
+        if (seg.token < 0) {
+            break;
+        }
         if (a.append && seg.last) {
             if constexpr (F16) {
                 append_row<_Float16, D>(a, seg);

@@ -993,7 +993,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
                 const int32_t key_end = std::min<int32_t>(row.keys, row.key_begin + static_cast<int32_t>(stop * kStepKeys));
                 const SynapseKvBatchToken& token = tokens[row.token];
                 segments.push_back(DecodeSegment{row.token, row.kv_head, key_begin, key_end, -1, row.list,
-                                                 stop == row.steps ? 1 : 0, token.slot, token.position, 0});
+                                                 stop == row.steps ? 1 : 0, token.slot, token.position, -1, -1, 0});
                 step = stop;
             }
             row.pieces = static_cast<int32_t>(segments.size() - row.first_segment);
@@ -1146,10 +1146,40 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     merges.insert(merges.end(), final_level.begin(), final_level.end());
     merges.insert(merges.end(), wide_level.begin(), wide_level.end());
 
+    // Segments as the decode kernel walks them: worker w's first segment at index w (no lookup before the wave's
+    // first descriptor read), its later ones after all workers' first ones, chained by `next`; each with the pool
+    // page of its first block from the host table (the same pages the step's table operations leave on the device),
+    // so the wave's first K/V requests need no table read either.
+    {
+        std::vector<DecodeSegment> chained(static_cast<size_t>(workers));
+        for (int32_t w = 0; w < workers; ++w) {
+            const int32_t begin = worker_segments[w];
+            const int32_t end = worker_segments[w + 1];
+            if (begin == end) {  // a worker without steps (not planned: workers never exceed the steps)
+                chained[w] = DecodeSegment{-1, 0, 0, 0, -1, -1, 0, 0, 0, -1, -1, 0};
+                continue;
+            }
+            int32_t previous = w;
+            chained[w] = segments[begin];
+            for (int32_t i = begin + 1; i < end; ++i) {
+                chained[previous].next = static_cast<int32_t>(chained.size());
+                previous = static_cast<int32_t>(chained.size());
+                chained.push_back(segments[i]);
+            }
+            chained[previous].next = -1;
+        }
+        for (DecodeSegment& seg : chained) {
+            if (seg.token >= 0 && seg.list < 0) {
+                seg.first_page = slot_page(cache, static_cast<uint32_t>(seg.slot),
+                                           static_cast<uint32_t>((seg.key_begin & ~(kStepKeys - 1)) / dims.page_tokens));
+            }
+        }
+        segments = std::move(chained);
+    }
     const size_t tokens_bytes = static_cast<size_t>(count) * sizeof(SynapseKvBatchToken);
     cache.tokens_offset = 0;
     cache.workers_offset = align_up(tokens_bytes, 256);
-    cache.members_offset = align_up(cache.workers_offset + worker_segments.size() * sizeof(int32_t), 256);
+    cache.members_offset = cache.workers_offset;
     cache.segments_offset = align_up(cache.members_offset + members.size() * sizeof(int32_t), 256);
     cache.merges_offset = align_up(cache.segments_offset + segments.size() * sizeof(DecodeSegment), 256);
     cache.prefill_offset = align_up(cache.merges_offset + merges.size() * sizeof(MergeItem), 256);
@@ -1185,7 +1215,6 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         staging = static_cast<uint8_t*>(cache.uploader.acquire(total));
     }
     std::memcpy(staging + cache.tokens_offset, tokens, tokens_bytes);
-    std::memcpy(staging + cache.workers_offset, worker_segments.data(), worker_segments.size() * sizeof(int32_t));
     std::memcpy(staging + cache.members_offset, members.data(), members.size() * sizeof(int32_t));
     std::memcpy(staging + cache.segments_offset, segments.data(), segments.size() * sizeof(DecodeSegment));
     std::memcpy(staging + cache.merges_offset, merges.data(), merges.size() * sizeof(MergeItem));
@@ -1512,7 +1541,6 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
     args.cosines = cache.cosines.pointer;
     args.sines = cache.sines.pointer;
     args.workers = cache.decode_workers;
-    args.worker_segments = reinterpret_cast<const int32_t*>(cache.step_blob + cache.workers_offset);
     args.members = reinterpret_cast<const int32_t*>(cache.step_blob + cache.members_offset);
     args.segments = reinterpret_cast<const DecodeSegment*>(cache.step_blob + cache.segments_offset);
     args.merges = reinterpret_cast<const MergeItem*>(cache.step_blob + cache.merges_offset);

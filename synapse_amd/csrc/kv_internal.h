@@ -68,9 +68,11 @@ struct DecodeSegment {
     int32_t last;      // 1: the segment ends at the token's own position (its wave appends the token)
     int32_t slot;      // the token's slot and position, copied from the step's tokens so that a wave starts with
     int32_t position;  // one descriptor read
-    int32_t reserved;
+    int32_t next;        // index of the same worker's next segment, -1 after its last (worker w's first is index w)
+    int32_t first_page;  // pool page of the segment's first 64-key block (-1: read it from the block table)
+    int32_t pad;
 };
-static_assert(sizeof(DecodeSegment) == 40, "DecodeSegment is 40 bytes");
+static_assert(sizeof(DecodeSegment) == 48, "DecodeSegment is 48 bytes");
 
 // The partial rows first_row .. first_row + count - 1 of one (token, KV head), merged into the output.
 struct MergeItem {
@@ -147,7 +149,6 @@ struct AttentionArgs {
     const float* cosines;
     const float* sines;
     int32_t workers;                 // decode wave workers
-    const int32_t* worker_segments;  // [workers + 1]: worker w walks segments [ws[w], ws[w + 1])
     const DecodeSegment* segments;
     const int32_t* members;  // step token indices of listed prefill items' columns
     const int32_t* lists;    // block lists of rows under KV page activation (DecodeSegment::list)
