@@ -360,6 +360,7 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
     const int32_t* table = geo.block_table + static_cast<size_t>(seg.slot) * geo.pages_per_slot;
     const int32_t* list = seg.list >= 0 ? a.lists + seg.list : nullptr;
     const int step_begin = seg.key_begin / kStepKeys;
+    const int step_end = (seg.key_end + kStepKeys - 1) / kStepKeys;
     half8 query[D / 32];
     Fragments16<D> first;
     if constexpr (PREFETCH) {
@@ -374,7 +375,7 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
     } else {
         load_query_f16<D>(a, seg.token, seg.position, seg.kv_head, query);
     }
-    attend_blocks_f16<D, PREFETCH>(a, table, seg.kv_head, step_begin, (seg.key_end + kStepKeys - 1) / kStepKeys, list,
+    attend_blocks_f16<D, PREFETCH>(a, table, seg.kv_head, step_begin, step_end, list,
                                    list != nullptr ? seg.position + 1 : seg.key_end, query, state, first);
 }
 
@@ -562,7 +563,10 @@ __device__ void append_row(const AttentionArgs& a, const DecodeSegment& seg) {
     const int lane = threadIdx.x & 63;
     const int logical = seg.position / geo.page_tokens;
     const int within = seg.position - logical * geo.page_tokens;
-    const int32_t page = load_uniform(geo.block_table + static_cast<size_t>(seg.slot) * geo.pages_per_slot + logical);
+    const int32_t page =
+        seg.append_page >= 0
+            ? seg.append_page
+            : load_uniform(geo.block_table + static_cast<size_t>(seg.slot) * geo.pages_per_slot + logical);
     T* base = reinterpret_cast<T*>(const_cast<uint8_t*>(geo.pool) + static_cast<uint64_t>(page) * geo.page_bytes);
     T* keys = base + region_offset(geo, 0, seg.kv_head);
     T* values = base + region_offset(geo, 1, seg.kv_head);

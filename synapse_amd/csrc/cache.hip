@@ -993,7 +993,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
                 const int32_t key_end = std::min<int32_t>(row.keys, row.key_begin + static_cast<int32_t>(stop * kStepKeys));
                 const SynapseKvBatchToken& token = tokens[row.token];
                 segments.push_back(DecodeSegment{row.token, row.kv_head, key_begin, key_end, -1, row.list,
-                                                 stop == row.steps ? 1 : 0, token.slot, token.position, -1, -1, 0});
+                                                 stop == row.steps ? 1 : 0, token.slot, token.position, -1, -1, -1});
                 step = stop;
             }
             row.pieces = static_cast<int32_t>(segments.size() - row.first_segment);
@@ -1156,7 +1156,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             const int32_t begin = worker_segments[w];
             const int32_t end = worker_segments[w + 1];
             if (begin == end) {  // a worker without steps (not planned: workers never exceed the steps)
-                chained[w] = DecodeSegment{-1, 0, 0, 0, -1, -1, 0, 0, 0, -1, -1, 0};
+                chained[w] = DecodeSegment{-1, 0, 0, 0, -1, -1, 0, 0, 0, -1, -1, -1};
                 continue;
             }
             int32_t previous = w;
@@ -1172,6 +1172,10 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
             if (seg.token >= 0 && seg.list < 0) {
                 seg.first_page = slot_page(cache, static_cast<uint32_t>(seg.slot),
                                            static_cast<uint32_t>((seg.key_begin & ~(kStepKeys - 1)) / dims.page_tokens));
+            }
+            if (seg.token >= 0 && seg.last != 0) {
+                seg.append_page = slot_page(cache, static_cast<uint32_t>(seg.slot),
+                                            static_cast<uint32_t>(seg.position) / dims.page_tokens);
             }
         }
         segments = std::move(chained);

@@ -69,8 +69,8 @@ struct DecodeSegment {
     int32_t slot;      // the token's slot and position, copied from the step's tokens so that a wave starts with
     int32_t position;  // one descriptor read
     int32_t next;        // index of the same worker's next segment, -1 after its last (worker w's first is index w)
-    int32_t first_page;  // pool page of the segment's first 64-key block (-1: read it from the block table)
-    int32_t pad;
+    int32_t first_page;   // pool page of the segment's first 64-key block (-1: read it from the block table)
+    int32_t append_page;  // with `last`: pool page of the token's own position (-1: read it from the block table)
 };
 static_assert(sizeof(DecodeSegment) == 48, "DecodeSegment is 48 bytes");
 
