@@ -414,6 +414,10 @@ def apply_options(args, cache) -> None:
         from synapse_amd.native import OPTION_SEGMENT_COST
 
         cache.set_option(OPTION_SEGMENT_COST, args.segment_cost)
+    if args.adaptive_split is not None:
+        from synapse_amd.native import OPTION_ADAPTIVE_SPLIT
+
+        cache.set_option(OPTION_ADAPTIVE_SPLIT, args.adaptive_split)
 
 
 def timed(torch, cache, run, repetitions, profile_every=1):
@@ -916,6 +920,10 @@ def config_decoder(args, torch) -> dict:
                 library.check(library.c_append_rope(cache, layer, rows.data_ptr(), width))
     torch.cuda.synchronize()
     log(f"KV filled: {model.kv_bytes / 2**30:.2f} GiB")
+    if args.adaptive_split is not None:
+        from synapse_amd.native import OPTION_ADAPTIVE_SPLIT
+
+        model.set_option(OPTION_ADAPTIVE_SPLIT, args.adaptive_split)
     rng = np.random.default_rng(SEED + 8)
     # The logits land in a reused pinned host buffer (the caller's buffer; a fresh pageable array per step would
     # time page faults and a staged copy).
@@ -984,6 +992,8 @@ def main() -> None:
     parser.add_argument("--prefill-split-keys", type=int, default=None, help="c5: keys per prefill work item")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--prefetch", type=int, default=None, help="decode kernel variant (0 or 1)")
+    parser.add_argument("--adaptive-split", type=int, default=None,
+                        help="SYNAPSE_KV_OPTION_ADAPTIVE_SPLIT: 1 weights decode shares by measured XCD speed")
     parser.add_argument("--segment-cost", type=int, default=None,
                         help="decode split: quarter key steps charged per row start in a worker's range")
     parser.add_argument("--separate", action="store_true",

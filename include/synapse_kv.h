@@ -52,6 +52,10 @@ extern "C" {
                                                separate reduce and split launches (same bits) */
 #define SYNAPSE_KV_OPTION_SEGMENT_COST 8u   /* decode work split: what a row start in a worker's range costs, in quarter
                                                key steps (0..64, default 8); a key step costs 4 */
+#define SYNAPSE_KV_OPTION_ADAPTIVE_SPLIT 9u /* 1: weight each decode worker's share of the steps by the measured speed of
+                                               its XCD (worker durations of earlier steps); attention outputs then
+                                               depend on timings in their last FP32 bits. 0 (default): equal shares,
+                                               results repeat bit for bit */
 
 /* GpuDeviceInfo (native/synapse-gpu/src/Features/GpuKernels/mod.rs:20-31), 152 bytes. */
 typedef struct SynapseKvDeviceInfo {

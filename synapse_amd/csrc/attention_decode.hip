@@ -30,7 +30,7 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = kDecodeBlockWaves;
 constexpr float kNegativeInfinity = -__builtin_inff();
 
 __device__ inline float fast_exp2(float value) { return __builtin_amdgcn_exp2f(value); }
@@ -598,6 +598,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
     if (worker >= a.workers) {
         return;
     }
+    const uint64_t started = a.timing != nullptr ? __builtin_amdgcn_s_memrealtime() : 0;
     // Worker w's first segment is segment w; the later ones follow `next`.
     for (int index = worker; index >= 0;) {
         const DecodeSegment seg = load_uniform(a.segments + index);
@@ -620,6 +621,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(AttentionArgs a) {
             attend_f32<D>(a, seg, state);
         }
         finish_segment<D, F16>(a, seg, state);
+    }
+    if (a.timing != nullptr && (threadIdx.x & 63) == 0) {
+        a.timing[worker] = static_cast<uint32_t>(__builtin_amdgcn_s_memrealtime() - started);
     }
 }
 

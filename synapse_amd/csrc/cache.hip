@@ -293,6 +293,45 @@ struct Dims {
 }  // namespace
 }  // namespace synapse_kv
 
+namespace synapse_kv {
+// Worker durations of a step's first kLaunches decode launches (SYNAPSE_KV_OPTION_ADAPTIVE_SPLIT): coherent pinned
+// memory the decode kernel writes through its device view (kWorkers entries per launch), the planned cost of each
+// worker, and an event after the last timed launch.
+struct SplitTiming {
+    static constexpr int kWorkers = 16384;
+    static constexpr int kLaunches = 4;
+    int launches = 0;            // timed launches of the step so far
+    uint32_t* host = nullptr;
+    uint32_t* device = nullptr;
+    hipEvent_t done = nullptr;
+    bool pending = false;        // launched, not yet read
+    std::vector<int64_t> costs;  // per worker of the timed plan
+
+    void allocate() {
+        if (host == nullptr) {
+            check_hip(hipHostMalloc(reinterpret_cast<void**>(&host), kLaunches * kWorkers * sizeof(uint32_t),
+                                    hipHostMallocMapped | hipHostMallocCoherent),
+                      "split timing buffer");
+            check_hip(hipHostGetDevicePointer(reinterpret_cast<void**>(&device), host, 0), "split timing address");
+            check_hip(hipEventCreateWithFlags(&done, hipEventDisableTiming), "split timing event");
+        }
+    }
+    void release() {
+        if (done != nullptr) {
+            (void)hipEventSynchronize(done);
+            (void)hipEventDestroy(done);
+            done = nullptr;
+        }
+        if (host != nullptr) {
+            (void)hipHostFree(host);
+            host = nullptr;
+            device = nullptr;
+        }
+        pending = false;
+    }
+};
+}  // namespace synapse_kv
+
 struct SynapseKvCache {
     synapse_kv::Dims dims{};
     int device = 0;
@@ -305,6 +344,12 @@ struct SynapseKvCache {
     uint32_t shared_prefix = 1;  // 1: decode reads copy-on-write pages shared by several step tokens once
     uint32_t fused_sums = 1;     // decoder: 1 adds deferred slice sums in the consuming kernels
     uint32_t segment_cost = 8;   // quarter key steps a decode worker's range pays for each row start in it
+    // Adaptive decode split: relative speed of each XCD's decode workers (1 = the mean), from timed launches.
+    uint32_t adaptive_split = 0;
+    double xcd_speed[synapse_kv::kXcds] = {1, 1, 1, 1, 1, 1, 1, 1};
+    synapse_kv::SplitTiming timing[2];
+    int timing_next = 0;     // buffer the next timed step uses
+    int timing_armed = -1;   // buffer the current step's first decode launch writes (-1: none)
     SynapseKvPageActivation activation{};  // KV page activation (enabled = 0: dense)
     synapse_kv::DeviceBuffer<uint8_t> summaries;  // per pool page: key minima and maxima of its activation pages
     uint64_t summary_page_bytes = 0;
@@ -392,6 +437,8 @@ struct SynapseKvCache {
         (void)hipStreamSynchronize(stream);
         uploader.release();
         pageable.release();
+        timing[0].release();
+        timing[1].release();
         for (auto& pair : event_pool) {
             (void)hipEventDestroy(pair.first);
             (void)hipEventDestroy(pair.second);
@@ -662,6 +709,58 @@ struct FixedMemory {
     uint8_t* base;
     size_t bytes;
 };
+
+// Adaptive split: folds the worker durations of finished timed launches into the XCD speeds (cost planned per
+// tick, per XCD, relative to the mean over the XCDs; a quarter of it enters the running estimate, kept within
+// 0.5-2).
+// The XCD of decode worker w's workgroup (the dispatcher places workgroup b on XCD b % kXcds).
+int worker_xcd(int w) { return (w / kDecodeBlockWaves) % kXcds; }
+
+// Adaptive split: folds the worker durations of finished timed launches into the XCD speeds. An XCD's speed is the
+// cost its workers were planned per tick, relative to the mean over the XCDs; half of each measurement enters the
+// running estimate, which stays within 0.5-2. (Per-workgroup speeds, which would follow each CU, measured no
+// better: the CUs' order changes from launch to launch, the XCDs' holds.)
+void update_xcd_speeds(SynapseKvCache& cache) {
+    for (SplitTiming& timing : cache.timing) {
+        if (!timing.pending) {
+            continue;
+        }
+        const hipError_t state = hipEventQuery(timing.done);
+        if (state == hipErrorNotReady) {
+            (void)hipGetLastError();
+            continue;
+        }
+        check_hip(state, "split timing");
+        timing.pending = false;
+        double cost[kXcds] = {};
+        double ticks[kXcds] = {};
+        for (int launch = 0; launch < timing.launches; ++launch) {
+            const uint32_t* durations = timing.host + static_cast<size_t>(launch) * SplitTiming::kWorkers;
+            for (size_t w = 0; w < timing.costs.size(); ++w) {
+                cost[worker_xcd(static_cast<int>(w))] += static_cast<double>(timing.costs[w]);
+                ticks[worker_xcd(static_cast<int>(w))] += static_cast<double>(durations[w]);
+            }
+        }
+        double mean = 0.0;
+        int measured = 0;
+        for (int x = 0; x < kXcds; ++x) {
+            if (cost[x] > 0.0 && ticks[x] > 0.0) {
+                mean += cost[x] / ticks[x];
+                ++measured;
+            }
+        }
+        if (measured == 0) {
+            continue;
+        }
+        mean /= measured;
+        for (int x = 0; x < kXcds; ++x) {
+            if (cost[x] > 0.0 && ticks[x] > 0.0) {
+                const double relative = cost[x] / ticks[x] / mean;
+                cache.xcd_speed[x] = std::min(2.0, std::max(0.5, 0.5 * cache.xcd_speed[x] + 0.5 * relative));
+            }
+        }
+    }
+}
 
 void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t count,
                const std::vector<uint32_t>& old_lengths, const FixedMemory* fixed = nullptr) {
@@ -939,6 +1038,7 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
     // Even split: the steps of all rows laid end to end, cut into equal shares for the resident wave workers (at
     // least split_keys keys each). A row cut by worker boundaries becomes several segments.
     std::vector<DecodeSegment> segments;
+    std::vector<int64_t> planned_costs;  // adaptive split: each worker's share of the cost
     auto split = [&](std::vector<Row>& list, int32_t resident, std::vector<int32_t>& worker_segments) -> int32_t {
         int64_t total_steps = 0;
         for (Row& row : list) {
@@ -973,7 +1073,24 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         // single segment of the same length).
         const int64_t cost = cache.segment_cost;
         const int64_t total_cost = 4 * total_steps + cost * static_cast<int64_t>(list.size());
-        auto boundary = [&](int64_t worker) { return worker * total_cost / workers; };
+        // With the adaptive split, worker w's share is proportional to its XCD's measured speed.
+        std::vector<int64_t> weights;
+        if (cache.adaptive_split != 0) {
+            weights.resize(static_cast<size_t>(workers) + 1, 0);
+            for (int32_t w = 0; w < workers; ++w) {
+                const double speed = cache.xcd_speed[worker_xcd(w)];
+                weights[w + 1] = weights[w] + static_cast<int64_t>(std::llround(speed * 65536.0));
+            }
+        }
+        auto boundary = [&](int64_t worker) {
+            return weights.empty() ? worker * total_cost / workers : total_cost * weights[worker] / weights[workers];
+        };
+        if (cache.adaptive_split != 0) {
+            planned_costs.resize(static_cast<size_t>(workers));
+            for (int32_t w = 0; w < workers; ++w) {
+                planned_costs[w] = boundary(w + 1) - boundary(w);
+            }
+        }
         int64_t worker = 0;
         int64_t row_cost = 0;  // cost position of the current row's start
         worker_segments.push_back(static_cast<int32_t>(segments.size()));
@@ -1005,7 +1122,16 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         return workers;
     };
     std::vector<int32_t> worker_segments;
+    update_xcd_speeds(cache);
     const int32_t workers = split(rows, cache.decode_waves, worker_segments);
+    cache.timing_armed = -1;
+    if (cache.adaptive_split != 0 && workers > 0 && workers <= SplitTiming::kWorkers &&
+        !cache.timing[cache.timing_next].pending) {
+        cache.timing_armed = cache.timing_next;
+        cache.timing[cache.timing_next].costs = std::move(planned_costs);
+        cache.timing[cache.timing_next].launches = 0;
+        cache.timing_next ^= 1;
+    }
 
     // Partial rows and merge entries. A row of its own that was cut gets consecutive partial rows. A shared set's
     // keys are cut, per KV head, into P listed prefill items of about equal length (enough items over all sets to
@@ -1595,8 +1721,20 @@ void run_attention(SynapseKvCache& cache, uint32_t layer, const float* qkv, uint
                                  prompt_items + listed_items, kPrefillTiles, fp16),
                   "prefill attention");
     }
+    const int timed = args.workers > 0 ? cache.timing_armed : -1;
+    if (timed >= 0) {
+        args.timing = cache.timing[timed].device + static_cast<size_t>(cache.timing[timed].launches) * SplitTiming::kWorkers;
+    }
     check_hip(launch_decode(launch_for(cache, SYNAPSE_KV_KERNEL_DECODE, args.workers > 0), args, fp16, cache.prefetch != 0),
               "decode attention");
+    if (timed >= 0) {
+        SplitTiming& timing = cache.timing[timed];
+        check_hip(hipEventRecord(timing.done, cache.stream), "split timing event");
+        timing.pending = true;
+        if (++timing.launches == SplitTiming::kLaunches) {
+            cache.timing_armed = -1;
+        }
+    }
     const int first_level = cache.first_level_merges;
     if (first_level > 0) {
         check_hip(launch_merge(launch_for(cache, SYNAPSE_KV_KERNEL_MERGE, true), args, 0, first_level, false),
@@ -1713,6 +1851,14 @@ int32_t synapse_kv_set_option(SynapseKvCache* cache, uint32_t option, uint32_t v
                 invalid("the segment cost is 0..64 quarter steps");
             }
             cache->segment_cost = value;
+        } else if (option == SYNAPSE_KV_OPTION_ADAPTIVE_SPLIT) {
+            if (value != 0) {
+                cache->timing[0].allocate();
+                cache->timing[1].allocate();
+            } else {
+                std::fill(std::begin(cache->xcd_speed), std::end(cache->xcd_speed), 1.0);
+            }
+            cache->adaptive_split = value != 0 ? 1 : 0;
         } else if (option == SYNAPSE_KV_OPTION_PREFILL_SPLIT_KEYS) {
             if (value % kStepKeys != 0) {
                 invalid("prefill split keys must be 0 (automatic) or a multiple of 64");

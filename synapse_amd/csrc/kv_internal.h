@@ -156,7 +156,13 @@ struct AttentionArgs {
     const PrefillItem* prefill;
     float* partial_out;  // [rows][group][head_dim]
     float* partial_ml;   // [rows][group][2] (maximum in log2 units, sum)
+    uint32_t* timing;    // non-null: worker w writes its duration (s_memrealtime ticks) to timing[w]
 };
+
+// Waves per decode workgroup: worker w runs in workgroup w / kDecodeBlockWaves, which the dispatcher places on XCD
+// (w / kDecodeBlockWaves) % kXcds.
+constexpr int kDecodeBlockWaves = 4;
+constexpr int kXcds = 8;
 
 struct GatherArgs {
     Geometry geo;

@@ -38,6 +38,7 @@ OPTION_PROFILE_EVERY = 5
 OPTION_SHARED_PREFIX = 6
 OPTION_FUSED_SUMS = 7
 OPTION_SEGMENT_COST = 8
+OPTION_ADAPTIVE_SPLIT = 9
 
 SELECT_KEY_BOUND = 0
 SELECT_RANDOM = 1

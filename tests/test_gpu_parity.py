@@ -267,6 +267,31 @@ def test_split_cost_extremes(torch_gpu, cost):
         pair.check_contents(slot)
 
 
+def test_adaptive_split(torch_gpu):
+    """SYNAPSE_KV_OPTION_ADAPTIVE_SPLIT: worker shares weighted by the XCD speeds measured on earlier steps' first
+    four decode launches. Consecutive decode steps over rows of very different lengths, fused and separate launches,
+    stay within the attention bar of the restatement while the weights move; the stored K/V stay bit-exact; turning
+    the option off restores equal shares."""
+    from synapse_amd.native import OPTION_ADAPTIVE_SPLIT
+
+    say("adaptive split")
+    pair = Pair(torch_gpu, heads=28, kv_heads=4, head_dim=128, max_positions=8192, growth=1024, max_pages=40,
+                layers=5, slots=3)
+    rng = np.random.default_rng(303)
+    lengths = [3000, 700, 64]
+    for slot, length in enumerate(lengths):
+        for first in range(0, length, 256):
+            assert pair.step([(slot, p) for p in range(first, min(length, first + 256))], rng, attend=False) == 0
+    pair.gpu.set_option(OPTION_ADAPTIVE_SPLIT, 1)
+    for index in range(10):
+        assert pair.step([(slot, lengths[slot]) for slot in range(3)], rng, fused=index % 3 != 2) == 0
+        lengths = [length + 1 for length in lengths]
+    pair.gpu.set_option(OPTION_ADAPTIVE_SPLIT, 0)
+    assert pair.step([(slot, lengths[slot]) for slot in range(3)], rng, fused=True) == 0
+    for slot in range(3):
+        pair.check_contents(slot)
+
+
 def test_single_position_and_page_boundaries(torch_gpu):
     say("page boundaries")
     pair = Pair(torch_gpu, page=64, growth=64, max_pages=64, heads=28, kv_heads=4, head_dim=128)
