@@ -10,7 +10,11 @@
 //
 // On the device every 32-value block is an MFMA k-depth, as for Q8_0 (q8_layout.h), with the same 16-row x 64-column
 // tiles [row tile][column chunk]:
-//   * Q6_K codes are int8 (q - 32), exactly Q8_0's tile layout (1 KiB per tile);
+//   * Q6_K codes stay six bits (768 bytes per tile): the low nibbles in Q4_K's 512-byte layout (lane l owns the 8
+//     bytes at l * 8, byte j holding column 8 g + j of the first block in its low nibble and of the second block in
+//     its high nibble), then the high bit pairs, lane l owning the 4 bytes at 512 + l * 4: byte i holds, in bits
+//     2 p .. 2 p + 1 with p = 2 b + w, column 4 w + i of block b. A lane turns its 12 bytes into four words of four
+//     biased codes q (0..63) with a shift, a mask and one shift-or per word (q6k_code_place);
 //   * Q4_K codes stay four bits: 512 bytes per tile, lane l = 16 g + r owns the 8 bytes at l * 8, byte j holding
 //     column 8 g + j of the chunk's first block (low nibble) and of its second block (high nibble) for row 16 t + r.
 //     That pairing is GGML's own (sub-blocks 2 p and 2 p + 1 share bytes), and a chunk is always one such pair
@@ -27,6 +31,7 @@
 //     80 bytes per tile chunk (0.078 B per weight) against 256 for FP32 factors.
 #pragma once
 
+#include <math.h>
 #include <stddef.h>
 #include <stdint.h>
 #include <string.h>
@@ -43,6 +48,7 @@ constexpr int kSuperBlockValues = 256;
 constexpr int kQ4KBlockBytes = 144;
 constexpr int kQ6KBlockBytes = 210;
 constexpr int kQ4KTileBytes = kQ8TileBytes / 2;
+constexpr int kQ6KTileBytes = kQ8TileBytes * 3 / 4;  // low nibbles (kQ4KTileBytes), then high bit pairs
 constexpr int kKTileScales = 64;        // factors per tile and chunk
 constexpr int kKSuperFactorBytes = 320;  // a tile's factor group per super-block: 4 x 64 bytes + 16 x 2 FP16
 constexpr int kKFactorBytes = kKSuperFactorBytes / 4;  // per tile chunk
@@ -63,7 +69,28 @@ inline uint64_t ggml_matrix_bytes(uint32_t encoding, uint64_t rows, uint64_t col
 }
 
 // Device bytes per tile and chunk: codes, then scales.
-inline size_t tile_code_bytes(uint32_t encoding) { return encoding == kEncodingQ4K ? kQ4KTileBytes : kQ8TileBytes; }
+inline size_t tile_code_bytes(uint32_t encoding) {
+    return encoding == kEncodingQ4K ? kQ4KTileBytes : (encoding == kEncodingQ6K ? kQ6KTileBytes : kQ8TileBytes);
+}
+
+// Where the six-bit code q (= code + 32) of Q6_K value (row, column) sits in a matrix's device codes: its low nibble
+// at byte `low`, bits low_shift .. + 3, and its high bit pair at byte `high`, bits high_shift .. + 1.
+SYNAPSE_Q8_HD inline void q6k_code_place(int chunks, int row, int column, int64_t& low, int& low_shift, int64_t& high,
+                                         int& high_shift) {
+    const int tile = row / kQ8TileRows;
+    const int r = row % kQ8TileRows;
+    const int chunk = column / kQ8ChunkColumns;
+    const int within = column % kQ8ChunkColumns;
+    const int block = within / kQ8BlockElements;
+    const int g = (within % kQ8BlockElements) / 8;
+    const int j = within % 8;
+    const int64_t base = (static_cast<int64_t>(tile) * chunks + chunk) * kQ6KTileBytes;
+    const int lane = 16 * g + r;
+    low = base + lane * 8 + j;
+    low_shift = 4 * block;
+    high = base + kQ4KTileBytes + lane * 4 + j % 4;
+    high_shift = 2 * (2 * block + j / 4);
+}
 inline size_t tile_scale_bytes(uint32_t encoding) {
     return is_kquant(encoding) ? kKFactorBytes : kQ8TileScales * sizeof(uint16_t);
 }
@@ -73,9 +100,13 @@ SYNAPSE_Q8_HD inline float kq_half(const uint8_t* p) {
 #if defined(__HIP_DEVICE_COMPILE__)
     return static_cast<float>(__builtin_bit_cast(_Float16, bits));
 #else
-    _Float16 value;
-    memcpy(&value, &bits, 2);
-    return static_cast<float>(value);
+    // IEEE binary16 to FP32, exact (host compilers without _Float16).
+    const int exponent = (bits >> 10) & 31;
+    const int mantissa = bits & 1023;
+    const float magnitude = exponent == 0    ? ldexpf(static_cast<float>(mantissa), -24)
+                            : exponent == 31 ? (mantissa != 0 ? NAN : INFINITY)
+                                             : ldexpf(static_cast<float>(mantissa + 1024), exponent - 25);
+    return (bits >> 15) != 0 ? -magnitude : magnitude;
 #endif
 }
 
@@ -160,7 +191,14 @@ inline void kq_repack(uint32_t encoding, const uint8_t* blocks, int rows, int co
                     const int code = kq_code(encoding, block, sub * 32 + l);
                     const int column = b * 32 + l;
                     if (encoding == kEncodingQ6K) {
-                        codes[q8_code_offset(chunks, row, column)] = static_cast<uint8_t>(static_cast<int8_t>(code));
+                        int64_t low = 0;
+                        int64_t high = 0;
+                        int low_shift = 0;
+                        int high_shift = 0;
+                        q6k_code_place(chunks, row, column, low, low_shift, high, high_shift);
+                        const int q = code + 32;
+                        codes[low] |= static_cast<uint8_t>((q & 0xF) << low_shift);
+                        codes[high] |= static_cast<uint8_t>((q >> 4) << high_shift);
                     } else {
                         // The Q8_0 offset of (row, column) with the block bit dropped, halved: lane * 8 + j.
                         const int tile = row / kQ8TileRows;

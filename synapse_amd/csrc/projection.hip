@@ -118,6 +118,12 @@ __device__ inline ChunkWeights<E> load_chunk(const uint8_t* codes, const void* s
     if constexpr (E == kEncodingQ4K) {
         const uintx2 half = __builtin_nontemporal_load(reinterpret_cast<const uintx2*>(codes + tile_chunk * kQ4KTileBytes) + lane);
         w.codes = uintx4{half.x, half.y, 0u, 0u};
+    } else if constexpr (E == kEncodingQ6K) {
+        // Low nibbles in .xy, high bit pairs in .z (q6k_codes turns them into biased codes).
+        const uint8_t* tile = codes + tile_chunk * kQ6KTileBytes;
+        const uintx2 low = __builtin_nontemporal_load(reinterpret_cast<const uintx2*>(tile) + lane);
+        const uint32_t high = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(tile + kQ4KTileBytes) + lane);
+        w.codes = uintx4{low.x, low.y, high, 0u};
     } else {
         w.codes = __builtin_nontemporal_load(reinterpret_cast<const uintx4*>(codes + tile_chunk * kQ8TileBytes) + lane);
     }
@@ -141,6 +147,12 @@ __device__ inline ChunkWeights<E> load_chunk(const uint8_t* codes, const void* s
             reinterpret_cast<const uint16_t*>(group + 4 * kKTileScales)[(4 * g + (lane & 3)) * 2 + ((lane >> 3) & 1)];
     }
     return w;
+}
+
+// Word 2 b + w of a loaded Q6_K chunk (ChunkWeights::codes): the biased codes q = code + 32 of columns 4 w .. 4 w + 3
+// of block b, one per byte (kquant_layout.h).
+__device__ inline uint32_t q6k_word(uintx4 codes, int b, int w) {
+    return ((codes[w] >> (4 * b)) & 0x0F0F0F0Fu) | (((codes[2] >> (2 * (2 * b + w))) & 0x03030303u) << 4);
 }
 
 // factors[n] = the value lane 16 g + n holds, for every lane of row group g (DPP row_newbcast:n).
@@ -167,6 +179,8 @@ __device__ inline void weight_fragments(uintx4 codes, bf16x8 (&weight)[2]) {
                 int code;
                 if constexpr (E == kEncodingQ4K) {
                     code = static_cast<int>((codes[w] >> (8 * i + 4 * b)) & 0xF);
+                } else if constexpr (E == kEncodingQ6K) {
+                    code = static_cast<int>((q6k_word(codes, b, w) >> (8 * i)) & 0xFF) - 32;
                 } else {
                     code = static_cast<int8_t>((codes[2 * b + w] >> (8 * i)) & 0xFF);
                 }
@@ -415,7 +429,7 @@ __global__ __launch_bounds__(kGemmWaves * 64, E == kEncodingQ6K ? 3 : 2) void pr
             tiles[r].codes = seg.codes + first_chunk * kQ8TileBytes;
             tiles[r].scales = static_cast<const uint16_t*>(seg.scales) + first_chunk * kQ8TileScales;
         } else {
-            tiles[r].codes = seg.codes + first_chunk * (E == kEncodingQ4K ? kQ4KTileBytes : kQ8TileBytes);
+            tiles[r].codes = seg.codes + first_chunk * (E == kEncodingQ4K ? kQ4KTileBytes : kQ6KTileBytes);
             tiles[r].scales = static_cast<const uint8_t*>(seg.scales) + (first_chunk >> 2) * kKSuperFactorBytes;
         }
         tiles[r].rows_left = global_tile < a.total_tiles ? seg.rows - local * kQ8TileRows : 0;
@@ -596,7 +610,8 @@ __device__ inline void codes_to_half(uint32_t word, uint32_t bias_xor, _Float16 
     out[at + 3] = second[1];
 }
 
-// The chunk's two blocks of A fragments in FP16: Q8_0 / Q6_K int8 codes, Q4_K nibbles (block 0 low, block 1 high).
+// The chunk's two blocks of A fragments in FP16: Q8_0 int8 codes, Q6_K six-bit codes biased by 32 (q6k_word), Q4_K
+// nibbles (block 0 low, block 1 high).
 template <uint32_t E>
 __device__ inline void weight_fragments_f16(uintx4 codes, halfx8 (&weight)[2]) {
 #pragma unroll
@@ -606,6 +621,8 @@ __device__ inline void weight_fragments_f16(uintx4 codes, halfx8 (&weight)[2]) {
             if constexpr (E == kEncodingQ4K) {
                 codes_to_half((codes[w] >> (4 * b)) & 0x0F0F0F0Fu, 0u, static_cast<_Float16>(1024.0f), weight[b],
                               4 * w);
+            } else if constexpr (E == kEncodingQ6K) {
+                codes_to_half(q6k_word(codes, b, w), 0u, static_cast<_Float16>(1056.0f), weight[b], 4 * w);
             } else {
                 codes_to_half(codes[2 * b + w], 0x80808080u, static_cast<_Float16>(1152.0f), weight[b], 4 * w);
             }

@@ -149,3 +149,72 @@ def test_q8_device_layout_is_a_bijection_and_round_trips(tmp_path):
                     str(binary)], check=True)
     result = subprocess.run([str(binary)], capture_output=True, text=True)
     assert result.returncode == 0, result.stdout
+
+
+Q6_LAYOUT_PROGRAM = r'''
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+#include "kquant_layout.h"
+using namespace synapse_kv;
+int main() {
+    int failures = 0;
+    for (int rows : {1, 16, 17, 40}) {
+        for (int columns : {256, 512, 768}) {
+            const int chunks = q8_chunks(columns);
+            const size_t size = (size_t)q8_tiles(rows) * chunks * kQ6KTileBytes;
+            std::vector<int> low_seen(size * 2, 0), high_seen(size * 4, 0);
+            const int supers = columns / 256;
+            std::vector<unsigned char> blocks((size_t)rows * supers * 210);
+            for (auto& b : blocks) { b = (unsigned char)(rand() & 0xFF); }
+            std::vector<unsigned char> codes(size), factors((size_t)q8_tiles(rows) * chunks * kKFactorBytes);
+            kq_repack(kEncodingQ6K, blocks.data(), rows, columns, codes.data(), factors.data());
+            for (int row = 0; row < rows; ++row) {
+                for (int column = 0; column < columns; ++column) {
+                    long long low = 0, high = 0;
+                    int low_shift = 0, high_shift = 0;
+                    int64_t l64 = 0, h64 = 0;
+                    q6k_code_place(chunks, row, column, l64, low_shift, h64, high_shift);
+                    low = l64;
+                    high = h64;
+                    if (low < 0 || low >= (long long)size || high < 0 || high >= (long long)size) { ++failures; continue; }
+                    if (low_seen[low * 2 + low_shift / 4]++ || high_seen[high * 4 + high_shift / 2]++) { ++failures; }
+                    const int q = ((codes[low] >> low_shift) & 15) | (((codes[high] >> high_shift) & 3) << 4);
+                    const unsigned char* block = blocks.data() + ((size_t)row * supers + column / 256) * 210;
+                    if (q != kq_code(kEncodingQ6K, block, column % 256) + 32) { ++failures; }
+                }
+            }
+            // Slots no value owns stay zero (row padding); every byte is either all nibbles or all pairs.
+            for (size_t byte = 0; byte < size; ++byte) {
+                const bool is_high = byte % kQ6KTileBytes >= (size_t)kQ4KTileBytes;
+                for (int s = 0; s < (is_high ? 4 : 2); ++s) {
+                    const int seen = is_high ? high_seen[byte * 4 + s] : low_seen[byte * 2 + s];
+                    const int bits = is_high ? (codes[byte] >> (2 * s)) & 3 : (codes[byte] >> (4 * s)) & 15;
+                    if (!seen && bits) { ++failures; }
+                }
+                if ((is_high ? low_seen[byte * 2] : high_seen[byte * 4]) != 0) { ++failures; }
+            }
+        }
+    }
+    // Row 3, column 64 + 32 + 8 * 2 + 5 of a 4-chunk matrix: tile 0, chunk 1 (bytes 768..), lane 16 * 2 + 3, byte 5
+    // of its nibbles (second block: high nibble), byte 1 of its pairs at p = 2 * 1 + 1.
+    int64_t low = 0, high = 0;
+    int low_shift = 0, high_shift = 0;
+    q6k_code_place(4, 3, 64 + 32 + 16 + 5, low, low_shift, high, high_shift);
+    if (low != 768 + 35 * 8 + 5 || low_shift != 4 || high != 768 + 512 + 35 * 4 + 1 || high_shift != 6) { ++failures; }
+    std::printf("%d\n", failures);
+    return failures != 0;
+}
+'''
+
+
+def test_q6_k_device_layout_holds_every_code_once(tmp_path):
+    """The six-bit Q6_K device layout (low nibbles, then high bit pairs): every value's two slots are distinct and
+    inside the matrix, they hold GGML's code + 32 for random super-blocks, and slots no value owns stay zero."""
+    source = tmp_path / "q6_layout.cpp"
+    source.write_text(Q6_LAYOUT_PROGRAM)
+    binary = tmp_path / "q6_layout"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", str(ROOT / "synapse_amd" / "csrc"), str(source), "-o",
+                    str(binary)], check=True)
+    result = subprocess.run([str(binary)], capture_output=True, text=True)
+    assert result.returncode == 0, result.stdout
