@@ -769,9 +769,10 @@ __global__ __launch_bounds__(kWaves * 64) void merge_kernel(AttentionArgs a, int
 }
 
 // Wide split merge: one workgroup of kWideWaves waves per (merge entry, query head, 64 dims) for rows of up to
-// 128 * kWideWaves splits. Wave w merges splits 128 w .. 128 w + 127 as merge_kernel does (one round of loads),
-// then wave 0 combines the waves' (max, sum, row) through LDS with the same rescaling: a row of any piece count up
-// to the limit takes one launch and about the latency of a 128-split merge.
+// 128 * kWideWaves splits. Wave w merges its share of about count / kWideWaves consecutive splits as merge_kernel
+// does (one round of loads), then wave 0 combines the waves' (max, sum, row) through LDS with the same rescaling: a
+// row of any piece count up to the limit takes one launch and about the latency of a merge of count / kWideWaves
+// splits.
 template <int D>
 __global__ __launch_bounds__(kWideWaves * 64) void merge_wide_kernel(AttentionArgs a, int first, int count) {
     __shared__ float rows[kWideWaves][64];
@@ -787,9 +788,11 @@ __global__ __launch_bounds__(kWideWaves * 64) void merge_wide_kernel(AttentionAr
     const MergeItem merge = load_uniform(a.merges + first + job / (group * chunks));
     const int head = (job / chunks) % group;
     const int chunk = job % chunks;
+    // The splits are shared out evenly: wave w takes `per` consecutive splits (at most 128).
+    const int per = (merge.count + kWideWaves - 1) / kWideWaves;
     MergeItem part = merge;
-    part.first_row = merge.first_row + 128 * wave;
-    part.count = min(128, max(0, merge.count - 128 * wave));
+    part.first_row = merge.first_row + per * wave;
+    part.count = min(per, max(0, merge.count - per * wave));
     float maximum = kNegativeInfinity;
     float sum = 0.0f;
     float value = 0.0f;
