@@ -379,7 +379,8 @@ __device__ void attend_f16(const AttentionArgs& a, const DecodeSegment& seg, Wav
                                    list != nullptr ? seg.position + 1 : seg.key_end, query, state, first);
 }
 
-// One token's segment for one KV head, FP32 pages.
+// One token's segment for one KV head, FP32 pages. The first step's K and V are requested right after the query's
+// loads (the plan carries the block's pool page), so the query and the first block are one round trip.
 template <int D>
 __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, WaveState<D>& state) {
     const Geometry& geo = a.geo;
@@ -389,8 +390,10 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
     // B operand of S^T = K Q^T for k-step (c, i): dim 16*c + 4*g + i of query head r. The RoPE partner of dim
     // i < D/2 sits in the same lane at c + D/32.
     floatx4 query[D / 16];
+    float cosines[D / 32][4];
+    float sines[D / 32][4];
+    const bool valid = r < geo.group;
     {
-        const bool valid = r < geo.group;
         const float* q = a.qkv + static_cast<size_t>(seg.token) * a.qkv_stride +
                          static_cast<size_t>(seg.kv_head * geo.group + (valid ? r : 0)) * D;
 #pragma unroll
@@ -398,25 +401,15 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
             query[c] = *reinterpret_cast<const floatx4*>(q + 16 * c + 4 * g);
         }
         if (a.rotate) {
-            const float* cosines = a.cosines + static_cast<size_t>(seg.position) * (D / 2);
-            const float* sines = a.sines + static_cast<size_t>(seg.position) * (D / 2);
+            const float* cos_row = a.cosines + static_cast<size_t>(seg.position) * (D / 2);
+            const float* sin_row = a.sines + static_cast<size_t>(seg.position) * (D / 2);
 #pragma unroll
             for (int c = 0; c < D / 32; ++c) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int index = 16 * c + 4 * g + i;
-                    float first;
-                    float second;
-                    rotate_pair(query[c][i], query[c + D / 32][i], cosines[index], sines[index], first, second);
-                    query[c][i] = first;
-                    query[c + D / 32][i] = second;
+                    cosines[c][i] = cos_row[16 * c + 4 * g + i];
+                    sines[c][i] = sin_row[16 * c + 4 * g + i];
                 }
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-            if (!valid) {
-                query[c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
             }
         }
     }
@@ -428,28 +421,25 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
     // 64-key block holding it is read, its other keys masked); keys at or past key_limit are masked.
     const int32_t* list = seg.list >= 0 ? a.lists + seg.list : nullptr;
     const int key_limit = list != nullptr ? seg.position + 1 : seg.key_end;
+    const int step_begin = seg.key_begin / kStepKeys;
     const int step_end = (seg.key_end + kStepKeys - 1) / kStepKeys;
 
-    for (int step = seg.key_begin / kStepKeys; step < step_end; ++step) {
+    // The step's K and V fragments are requested together: one memory round trip per step.
+    floatx4 key_fragment[4][D / 16];
+    floatx4 value_fragment[4][D / 16];
+    auto fetch = [&](int step) __attribute__((always_inline)) {
         const int entry = list != nullptr ? load_uniform(list + step) : step * kStepKeys;
         const int key0 = entry & ~(kStepKeys - 1);
-        const int key_low = list != nullptr ? entry : 0;
-        const int key_end = list != nullptr ? min(entry + geo.summary_keys, key_limit) : key_limit;
         const int logical = key0 / page_tokens;
         const int within = key0 - logical * page_tokens;
         // The first step's page comes with the plan (no table read before the wave's first request).
         const int page_index =
-            step == seg.key_begin / kStepKeys && list == nullptr && seg.first_page >= 0 ? seg.first_page
-                                                                                       : load_uniform(table + logical);
+            step == step_begin && list == nullptr && seg.first_page >= 0 ? seg.first_page : load_uniform(table + logical);
         const float* page = reinterpret_cast<const float*>(geo.pool + static_cast<uint64_t>(page_index) * geo.page_bytes);
         const floatx4* keys =
             reinterpret_cast<const floatx4*>(page + key_region + static_cast<size_t>(within) * D) + lane;
         const floatx4* values =
             reinterpret_cast<const floatx4*>(page + value_region + static_cast<size_t>(within) * D) + lane;
-
-        // The step's K and V fragments are requested together: one memory round trip per step.
-        floatx4 key_fragment[4][D / 16];
-        floatx4 value_fragment[4][D / 16];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -464,8 +454,12 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
                 value_fragment[t][mt] = load_fragment(values + (t * (D / 16) + mt) * 64);
             }
         }
-        // Keeps the scheduler from sinking the loads towards their uses (which would serialize the round trips).
-        __builtin_amdgcn_sched_barrier(0);
+        return entry;
+    };
+    auto compute = [&](int entry) __attribute__((always_inline)) {
+        const int key0 = entry & ~(kStepKeys - 1);
+        const int key_low = list != nullptr ? entry : 0;
+        const int key_end = list != nullptr ? min(entry + geo.summary_keys, key_limit) : key_limit;
         floatx4 scores[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -506,6 +500,35 @@ __device__ void attend_f32(const AttentionArgs& a, const DecodeSegment& seg, Wav
                 }
             }
         }
+    };
+
+    // Keeps the scheduler from sinking the loads towards their uses (which would serialize the round trips).
+    int entry = fetch(step_begin);
+    __builtin_amdgcn_sched_barrier(0);
+    if (a.rotate) {
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float first;
+                float second;
+                rotate_pair(query[c][i], query[c + D / 32][i], cosines[c][i], sines[c][i], first, second);
+                query[c][i] = first;
+                query[c + D / 32][i] = second;
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+        if (!valid) {
+            query[c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
+    compute(entry);
+    for (int step = step_begin + 1; step < step_end; ++step) {
+        entry = fetch(step);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(entry);
     }
 }
 
