@@ -128,7 +128,8 @@ __device__ inline ChunkWeights<E> load_chunk(const uint8_t* codes, const void* s
         w.codes = __builtin_nontemporal_load(reinterpret_cast<const uintx4*>(codes + tile_chunk * kQ8TileBytes) + lane);
     }
     if constexpr (E == kEncodingQ8_0 && kWide) {
-        w.scales = reinterpret_cast<const uintx4*>(static_cast<const uint16_t*>(scales) + tile_chunk * kQ8TileScales)[g];
+        w.scales = __builtin_nontemporal_load(
+            reinterpret_cast<const uintx4*>(static_cast<const uint16_t*>(scales) + tile_chunk * kQ8TileScales) + g);
     } else if constexpr (E == kEncodingQ8_0) {
         // Row group g's eight scales (q8_scale_offset: [g][block][row % 4]) are four 32-bit words.
         w.factor = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(scales) + tile_chunk * kQ8TileScales)
