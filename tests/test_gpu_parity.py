@@ -267,16 +267,17 @@ def test_split_cost_extremes(torch_gpu, cost):
         pair.check_contents(slot)
 
 
-def test_adaptive_split(torch_gpu):
+@pytest.mark.parametrize("precision", ["f16", "f32"])
+def test_adaptive_split(torch_gpu, precision):
     """SYNAPSE_KV_OPTION_ADAPTIVE_SPLIT: worker shares weighted by the XCD speeds measured on earlier steps' first
     four decode launches. Consecutive decode steps over rows of very different lengths, fused and separate launches,
     stay within the attention bar of the restatement while the weights move; the stored K/V stay bit-exact; turning
     the option off restores equal shares."""
     from synapse_amd.native import OPTION_ADAPTIVE_SPLIT
 
-    say("adaptive split")
+    say("adaptive split", precision)
     pair = Pair(torch_gpu, heads=28, kv_heads=4, head_dim=128, max_positions=8192, growth=1024, max_pages=40,
-                layers=5, slots=3)
+                layers=5, slots=3, precision=precision, page=256 if precision == "f16" else 128)
     rng = np.random.default_rng(303)
     lengths = [3000, 700, 64]
     for slot, length in enumerate(lengths):
