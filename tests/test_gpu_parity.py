@@ -277,7 +277,7 @@ def test_adaptive_split(torch_gpu, precision):
 
     say("adaptive split", precision)
     pair = Pair(torch_gpu, heads=28, kv_heads=4, head_dim=128, max_positions=8192, growth=1024, max_pages=40,
-                layers=5, slots=3, precision=precision, page=256 if precision == "f16" else 128)
+                layers=5, slots=3, precision=precision)
     rng = np.random.default_rng(303)
     lengths = [3000, 700, 64]
     for slot, length in enumerate(lengths):
