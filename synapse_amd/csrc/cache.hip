@@ -1071,7 +1071,13 @@ void plan_step(SynapseKvCache& cache, const SynapseKvBatchToken* tokens, int32_t
         // worker's range costs segment_cost more (its query, RoPE and first block are not overlapped with the
         // previous segment's steps: on C3 a worker with two segments ends about one step later than one with a
         // single segment of the same length).
-        const int64_t cost = cache.segment_cost;
+        // With fewer than four steps per worker the row-start cost only misplaces whole steps: a share of a little
+        // more than one step leaves the workers at row starts empty and gives a few others two steps, which then
+        // set the launch's length (C1: four of 130 workers). Such splits are even in steps, unless their rows are
+        // longer than the 512 pieces a wide merge takes in one round of loads per wave (C2's 513-step rows: the
+        // uneven split happens to keep them at 511 pieces, and one more measured slower in the merge).
+        const int64_t cost =
+            total_steps < 4 * static_cast<int64_t>(workers) && longest <= 64 * kWideWaves ? 0 : cache.segment_cost;
         const int64_t total_cost = 4 * total_steps + cost * static_cast<int64_t>(list.size());
         // With the adaptive split, worker w's share is proportional to its XCD's measured speed.
         std::vector<int64_t> weights;
