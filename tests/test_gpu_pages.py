@@ -342,3 +342,20 @@ def test_many_candidates_take_the_sort(torch_gpu, activation_page, budget):
     pair.activate(budget, 64, page_tokens=activation_page)
     pair.run([(0, length), (1, 3000)], rng, expect_sparse=True)
     pair.run([(0, length + 1), (1, 3001)], rng, fused=True, expect_sparse=True)
+
+
+def test_page_activation_under_the_adaptive_split(torch_gpu):
+    """Listed rows (KV page activation) split by measured XCD speeds (SYNAPSE_KV_OPTION_ADAPTIVE_SPLIT): several
+    steps, so the weights move, each against the restatement's sparse attention."""
+    from synapse_amd.native import OPTION_ADAPTIVE_SPLIT
+
+    say("page activation, adaptive split")
+    pair = PagePair(torch_gpu, heads=28, kv_heads=4, head_dim=128, precision="f16", page=64, growth=256,
+                    max_positions=2048, slots=4, max_pages=2048 // 64 * 4 + 8)
+    rng = np.random.default_rng(505)
+    prefill(pair, rng, [(0, 1500), (1, 700), (2, 1100)])
+    pair.gpu.set_option(OPTION_ADAPTIVE_SPLIT, 1)
+    pair.activate(6, 128, selection="key_bound")
+    for step in range(8):
+        pair.run([(0, 1500 + step), (1, 700 + step), (2, 1100 + step)], rng, fused=step % 2 == 0, expect_sparse=True)
+    pair.check_contents(0)
