@@ -710,9 +710,6 @@ struct FixedMemory {
     size_t bytes;
 };
 
-// Adaptive split: folds the worker durations of finished timed launches into the XCD speeds (cost planned per
-// tick, per XCD, relative to the mean over the XCDs; a quarter of it enters the running estimate, kept within
-// 0.5-2).
 // The XCD of decode worker w's workgroup (the dispatcher places workgroup b on XCD b % kXcds).
 int worker_xcd(int w) { return (w / kDecodeBlockWaves) % kXcds; }
 
