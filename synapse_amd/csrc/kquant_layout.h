@@ -100,13 +100,19 @@ SYNAPSE_Q8_HD inline float kq_half(const uint8_t* p) {
 #if defined(__HIP_DEVICE_COMPILE__)
     return static_cast<float>(__builtin_bit_cast(_Float16, bits));
 #else
-    // IEEE binary16 to FP32, exact (host compilers without _Float16).
-    const int exponent = (bits >> 10) & 31;
-    const int mantissa = bits & 1023;
-    const float magnitude = exponent == 0    ? ldexpf(static_cast<float>(mantissa), -24)
-                            : exponent == 31 ? (mantissa != 0 ? NAN : INFINITY)
-                                             : ldexpf(static_cast<float>(mantissa + 1024), exponent - 25);
-    return (bits >> 15) != 0 ? -magnitude : magnitude;
+    // IEEE binary16 to FP32, exact (host compilers without _Float16): subnormals scaled, the rest rebuilt as bits
+    // (exponent rebiased by 112, infinities and NaNs kept), so no float arithmetic meets a non-finite value.
+    const uint32_t sign = static_cast<uint32_t>(bits >> 15) << 31;
+    const uint32_t exponent = (bits >> 10) & 31;
+    const uint32_t mantissa = bits & 1023;
+    if (exponent == 0) {
+        const float magnitude = ldexpf(static_cast<float>(mantissa), -24);
+        return sign != 0 ? -magnitude : magnitude;
+    }
+    const uint32_t word = sign | ((exponent == 31 ? 255 : exponent + 112) << 23) | (mantissa << 13);
+    float value;
+    memcpy(&value, &word, 4);
+    return value;
 #endif
 }
 

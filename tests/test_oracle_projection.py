@@ -218,3 +218,34 @@ def test_q6_k_device_layout_holds_every_code_once(tmp_path):
                     str(binary)], check=True)
     result = subprocess.run([str(binary)], capture_output=True, text=True)
     assert result.returncode == 0, result.stdout
+
+
+HALF_PROGRAM = r'''
+#include <cstdio>
+#include "kquant_layout.h"
+int main() {
+    for (unsigned bits = 0; bits < 65536; ++bits) {
+        const unsigned char p[2] = {(unsigned char)(bits & 0xFF), (unsigned char)(bits >> 8)};
+        const float value = synapse_kv::kq_half(p);
+        unsigned word;
+        memcpy(&word, &value, 4);
+        printf("%08x\n", word);
+    }
+    return 0;
+}
+'''
+
+
+def test_host_half_conversion_matches_numpy_for_every_bit_pattern(tmp_path):
+    """kq_half's host branch (used by the weight repack on the CPU) rebuilds FP16 factors as FP32 bits; for all
+    65,536 patterns it must equal numpy's float16 -> float32 widening, NaN payloads, infinities and signed
+    subnormals included."""
+    source = tmp_path / "half.cpp"
+    source.write_text(HALF_PROGRAM)
+    binary = tmp_path / "half"
+    subprocess.run(["g++", "-std=c++17", "-O2", "-I", str(ROOT / "synapse_amd" / "csrc"), str(source), "-o",
+                    str(binary)], check=True)
+    result = subprocess.run([str(binary)], capture_output=True, text=True, check=True)
+    got = np.array([int(line, 16) for line in result.stdout.split()], dtype=np.uint32)
+    expected = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32).view(np.uint32)
+    assert got.shape == expected.shape and np.array_equal(got, expected)
